@@ -1,0 +1,157 @@
+"""batch_topk for AMD Instinct MI355X (gfx950).
+
+Python mirror of the reference host API (reference include/batch_topk.cuh:10-21) over the
+C ABI of ``libbatch_topk_amd.so`` (declared in include/batch_topk.h).  The functions keep
+the reference's names, argument order and meaning, and its error behaviour: they return a
+hipError_t code (0 success, 1 = hipErrorInvalidValue for a rejected argument).  Pointers
+are plain integers (device addresses); ``stream`` is a hipStream_t handle (0 = null stream).
+
+``topk`` and ``segmented_topk`` are torch conveniences built on the same C ABI: torch
+provides device memory and the stream, the HIP kernels do the work.  There is no CPU
+fallback: if the library is missing every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libbatch_topk_amd.so")
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+MAX_K = 1024
+PAD_INDEX = -1
+PAD_VALUE_BITS = 0xFFFF
+
+# Every extern "C" symbol declared in include/batch_topk.h.
+EXPORTED_SYMBOLS = (
+    "radix_topk_batch_topk_half",
+    "radix_topk_batch_topk_half_workspace_size",
+    "radix_topk_batch_topk_half_segmented",
+    "radix_topk_batch_topk_half_segmented_workspace_size",
+)
+
+_lib = None
+
+
+class TopkError(RuntimeError):
+    """A nonzero hipError_t returned by the engine."""
+
+    def __init__(self, code: int, what: str):
+        super().__init__(f"{what} failed with hipError_t {code}")
+        self.code = code
+
+
+def load_library():
+    """Load the in-tree HIP engine; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the HIP engine with `python -m batch_topk_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        L.radix_topk_batch_topk_half.restype = i32
+        L.radix_topk_batch_topk_half.argtypes = [vp, i32, i32, i32, vp, vp, vp, sz, vp]
+        L.radix_topk_batch_topk_half_workspace_size.restype = sz
+        L.radix_topk_batch_topk_half_workspace_size.argtypes = [i32, i32, i32]
+        L.radix_topk_batch_topk_half_segmented.restype = i32
+        L.radix_topk_batch_topk_half_segmented.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, sz, vp]
+        L.radix_topk_batch_topk_half_segmented_workspace_size.restype = sz
+        L.radix_topk_batch_topk_half_segmented_workspace_size.argtypes = [i32, i32, i32]
+        _lib = L
+    return _lib
+
+
+# ------------------------------------------------------------------ reference-shaped API
+
+def batch_topk_half(d_input: int, seg_num: int, seg_len: int, k: int, d_output_values: int,
+                    d_output_indices: int, d_workspace: int, workspace_bytes: int,
+                    stream: int = 0) -> int:
+    """reference include/batch_topk.cuh:10-19 -> hipError_t code."""
+    return int(load_library().radix_topk_batch_topk_half(
+        d_input, seg_num, seg_len, k, d_output_values, d_output_indices, d_workspace,
+        workspace_bytes, stream))
+
+
+def batch_topk_half_workspace_size(seg_num: int, seg_len: int, k: int) -> int:
+    """reference include/batch_topk.cuh:21 -> bytes (0 for an unsupported shape)."""
+    return int(load_library().radix_topk_batch_topk_half_workspace_size(seg_num, seg_len, k))
+
+
+def batch_topk_half_segmented(d_input: int, d_offsets: int, seg_num: int, max_seg_len: int,
+                              k: int, d_output_values: int, d_output_indices: int,
+                              d_workspace: int, workspace_bytes: int, stream: int = 0) -> int:
+    """Variable-length segments given by a device int32 offset array -> hipError_t code."""
+    return int(load_library().radix_topk_batch_topk_half_segmented(
+        d_input, d_offsets, seg_num, max_seg_len, k, d_output_values, d_output_indices,
+        d_workspace, workspace_bytes, stream))
+
+
+def batch_topk_half_segmented_workspace_size(seg_num: int, max_seg_len: int, k: int) -> int:
+    return int(load_library().radix_topk_batch_topk_half_segmented_workspace_size(
+        seg_num, max_seg_len, k))
+
+
+# ------------------------------------------------------------------ torch conveniences
+
+def _stream_handle(stream) -> int:
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def topk(x, k: int, workspace=None, stream=None):
+    """Top-k of every row of a contiguous fp16 CUDA tensor [seg_num, seg_len].
+
+    Returns (values fp16 [seg_num, k], indices int32 [seg_num, k]).  ``workspace`` may be a
+    uint8 CUDA tensor of at least ``batch_topk_half_workspace_size`` bytes.
+    """
+    import torch
+
+    if x.dtype != torch.float16 or x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
+        raise ValueError("topk expects a contiguous 2-D float16 CUDA tensor")
+    seg_num, seg_len = x.shape
+    ws_bytes = batch_topk_half_workspace_size(seg_num, seg_len, k)
+    if ws_bytes == 0:
+        raise TopkError(HIP_ERROR_INVALID_VALUE, "batch_topk_half_workspace_size")
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    vals = torch.empty((seg_num, k), dtype=torch.float16, device=x.device)
+    idx = torch.empty((seg_num, k), dtype=torch.int32, device=x.device)
+    rc = batch_topk_half(x.data_ptr(), seg_num, seg_len, k, vals.data_ptr(), idx.data_ptr(),
+                         workspace.data_ptr(), workspace.numel(), _stream_handle(stream))
+    if rc != HIP_SUCCESS:
+        raise TopkError(rc, "batch_topk_half")
+    return vals, idx
+
+
+def segmented_topk(x, offsets, k: int, max_seg_len: int, workspace=None, stream=None):
+    """Top-k of every segment x[offsets[s]:offsets[s+1]] of a 1-D fp16 CUDA tensor.
+
+    ``offsets`` is an int32 CUDA tensor of seg_num + 1 entries.  Ranks beyond a segment's
+    length hold index -1 and value bits 0xFFFF.
+    """
+    import torch
+
+    if x.dtype != torch.float16 or not x.is_cuda or not x.is_contiguous():
+        raise ValueError("segmented_topk expects a contiguous float16 CUDA tensor")
+    if offsets.dtype != torch.int32 or not offsets.is_cuda or offsets.dim() != 1:
+        raise ValueError("offsets must be a 1-D int32 CUDA tensor")
+    seg_num = offsets.numel() - 1
+    ws_bytes = batch_topk_half_segmented_workspace_size(seg_num, max_seg_len, k)
+    if ws_bytes == 0:
+        raise TopkError(HIP_ERROR_INVALID_VALUE, "batch_topk_half_segmented_workspace_size")
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    vals = torch.empty((seg_num, k), dtype=torch.float16, device=x.device)
+    idx = torch.empty((seg_num, k), dtype=torch.int32, device=x.device)
+    rc = batch_topk_half_segmented(x.data_ptr(), offsets.data_ptr(), seg_num, max_seg_len, k,
+                                   vals.data_ptr(), idx.data_ptr(), workspace.data_ptr(),
+                                   workspace.numel(), _stream_handle(stream))
+    if rc != HIP_SUCCESS:
+        raise TopkError(rc, "batch_topk_half_segmented")
+    return vals, idx

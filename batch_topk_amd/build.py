@@ -1,0 +1,52 @@
+"""Compile the HIP engine into batch_topk_amd/libbatch_topk_amd.so (gfx950 only).
+
+Run as ``python -m batch_topk_amd.build``; ``__graft_entry__.build()`` calls ``build()``.
+The library is built in-tree so that it travels with the source tree.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB_NAME = "libbatch_topk_amd.so"
+LIB_PATH = os.path.join(HERE, LIB_NAME)
+
+SOURCES = ["topk_kernels.hip", "api.cpp"]
+
+# -packed-fp32-ops: no v_pk_*_f32 in any code object (this engine has no fp32 math anyway).
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found; the HIP engine cannot be built")
+    return path
+
+
+def build(verbose: bool = False) -> str:
+    """Always recompiles (the build check must exercise the compiler)."""
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), *HIP_FLAGS, "-shared", "-o", tmp,
+           *[os.path.join(CSRC, s) for s in SOURCES], "-lamdhip64"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed to build " + LIB_NAME)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,179 @@
+// Host side of the batched fp16 top-k engine: argument validation, launch planning,
+// workspace carve and the C ABI declared in include/batch_topk.h.
+//
+// Validation runs before any HIP call, so every rejected argument returns
+// hipErrorInvalidValue (1) even on a machine without a GPU (reference behaviour:
+// src/batch_topk.cu:13-33,51-60).  The plan depends only on (seg_num, segment length, k),
+// so the workspace size is pure host arithmetic (reference src/batch_topk.cu:35-40).
+
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
+#include <chrono>
+#include <cstdint>
+#include <random>
+
+#include "../../include/batch_topk.h"
+#include "topk_common.hpp"
+
+namespace radix_topk_amd {
+namespace {
+
+constexpr int kMaxK = RADIX_TOPK_MAX_K;
+constexpr int kMaxCandArea = 4096;  // LDS entries (8 B each) of the candidate / merge area
+constexpr size_t kAlign = 256;
+constexpr int kInvalid = static_cast<int>(hipErrorInvalidValue);
+
+int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Launch plan for segments of at most `max_len` elements (plus up to 7 elements of
+// misalignment of the 16-byte load grid), `seg_num` segments and `k` outputs each.
+Plan make_plan(int seg_num, int64_t max_len, int k) {
+  Plan plan{};
+  plan.ok = false;
+  if (seg_num <= 0 || k <= 0 || k > kMaxK || max_len < 0) return plan;
+  // Threads per workgroup grow with k so that each wave's share of k stays well below its
+  // 64 lanes (the threshold step picks the ceil(k / waves)-th best lane of every wave).
+  const int block = k <= 64 ? 256 : (k <= 128 ? 512 : 1024);
+  const int64_t span = max_len + 7;  // worst-case aligned span of one segment
+  int vpt = 8;
+  for (int cand : {2, 4, 8}) {
+    if (static_cast<int64_t>(block) * cand * 8 >= span) {
+      vpt = cand;
+      break;
+    }
+  }
+  const int chunk = block * vpt * 8;
+  const int64_t W = span <= chunk ? 1 : (span + chunk - 1) / chunk;
+  const int kpad = next_pow2(k < 64 ? 64 : k);
+  const int cap_chunk = 2 * kpad > 2048 ? 2 * kpad : 2048;
+  const int cap_list = W > 1 ? (2 * kpad > 256 ? 2 * kpad : 256) : 0;
+  const int64_t merge_area = W * static_cast<int64_t>(cap_list);
+  const int64_t cand_area = merge_area > cap_chunk ? merge_area : cap_chunk;
+  if (cand_area > kMaxCandArea) return plan;  // segment too long for the fused merge
+  if (static_cast<int64_t>(seg_num) * W > 0x7fffffff) return plan;
+
+  plan.shape = KernelShape{block, vpt};
+  plan.chunk = chunk;
+  plan.W = static_cast<int>(W);
+  plan.cap_chunk = cap_chunk;
+  plan.cap_list = cap_list;
+  plan.cand_area = static_cast<int>(cand_area);
+  plan.kpad = kpad;
+  plan.lds_bytes = 256 * 4 + 16 * 4 + 16 * 4 + static_cast<size_t>(cand_area) * 8 +
+                   static_cast<size_t>(kpad) * 8 + static_cast<size_t>(kpad) * 4;
+  size_t ws = kAlign;                                   // alignment slack of the carve
+  ws += align_up(static_cast<size_t>(seg_num) * 8, kAlign);  // arrival tickets
+  if (W > 1) {
+    ws += align_up(static_cast<size_t>(seg_num) * W * 4, kAlign);             // list counts
+    ws += static_cast<size_t>(seg_num) * W * static_cast<size_t>(cap_list) * 8;  // lists
+  }
+  plan.ws_bytes = ws;
+  plan.ok = true;
+  return plan;
+}
+
+// Process-wide source of 48-bit call tokens for the arrival counters.  Tokens never repeat
+// within a process, start at a random point, and skip values whose six bytes are all equal
+// (the shape of a memset-poisoned workspace word).
+uint64_t next_epoch() {
+  static std::atomic<uint64_t> counter{[] {
+    std::random_device rd;
+    const uint64_t t = static_cast<uint64_t>(
+        std::chrono::steady_clock::now().time_since_epoch().count());
+    return ((static_cast<uint64_t>(rd()) << 32) ^ static_cast<uint64_t>(rd()) ^ (t * 0x9E3779B97F4A7C15ull));
+  }()};
+  for (;;) {
+    const uint64_t e = counter.fetch_add(1, std::memory_order_relaxed) & 0xFFFFFFFFFFFFull;
+    const uint64_t b = e & 0xff;
+    if (e == 0 || e == b * 0x010101010101ull) continue;
+    return e;
+  }
+}
+
+int run(const Plan& plan, const uint16_t* d_input, const int32_t* d_offsets, int seg_num,
+        int64_t seg_len, int64_t max_len, int k, uint16_t* d_values, int32_t* d_indices, void* d_workspace,
+        size_t workspace_bytes, void* stream) {
+  if (!plan.ok || workspace_bytes < plan.ws_bytes) return kInvalid;
+  const uintptr_t in_addr = reinterpret_cast<uintptr_t>(d_input);
+  if ((in_addr & 1u) || (reinterpret_cast<uintptr_t>(d_values) & 1u) ||
+      (reinterpret_cast<uintptr_t>(d_indices) & 3u) || (reinterpret_cast<uintptr_t>(d_offsets) & 3u)) {
+    return kInvalid;
+  }
+  TopkParams p{};
+  p.base = reinterpret_cast<const uint16_t*>(in_addr & ~static_cast<uintptr_t>(15));
+  p.elem0 = static_cast<int64_t>((in_addr & 15u) >> 1);
+  p.offsets = d_offsets;
+  p.seg_len = seg_len;
+  p.max_len = max_len;
+  p.seg_num = seg_num;
+  p.k = k;
+  p.chunks_per_seg = plan.W;
+  p.cap_chunk = plan.cap_chunk;
+  p.cap_list = plan.cap_list;
+  p.cand_area = plan.cand_area;
+  p.kpad = plan.kpad;
+  p.out_vals = d_values;
+  p.out_idx = d_indices;
+  const uintptr_t ws = align_up(reinterpret_cast<uintptr_t>(d_workspace), kAlign);
+  size_t off = 0;
+  p.tickets = reinterpret_cast<unsigned long long*>(ws + off);
+  off += align_up(static_cast<size_t>(seg_num) * 8, kAlign);
+  if (plan.W > 1) {
+    p.list_counts = reinterpret_cast<int32_t*>(ws + off);
+    off += align_up(static_cast<size_t>(seg_num) * plan.W * 4, kAlign);
+    p.lists = reinterpret_cast<unsigned long long*>(ws + off);
+  }
+  p.epoch = next_epoch();
+  return launch_segmented_topk(plan, p, stream);
+}
+
+}  // namespace
+}  // namespace radix_topk_amd
+
+using radix_topk_amd::kInvalid;
+using radix_topk_amd::make_plan;
+
+extern "C" {
+
+size_t radix_topk_batch_topk_half_workspace_size(int seg_num, int seg_len, int k) {
+  if (seg_num <= 0 || seg_len <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K || k > seg_len) return 0;
+  const radix_topk_amd::Plan plan = make_plan(seg_num, seg_len, k);
+  return plan.ok ? plan.ws_bytes : 0;
+}
+
+int radix_topk_batch_topk_half(const uint16_t* d_input, int seg_num, int seg_len, int k,
+                               uint16_t* d_output_values, int32_t* d_output_indices,
+                               void* d_workspace, size_t workspace_bytes, void* stream) {
+  if (seg_num <= 0 || seg_len <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K || k > seg_len) return kInvalid;
+  if (!d_input || !d_output_values || !d_output_indices || !d_workspace) return kInvalid;
+  const radix_topk_amd::Plan plan = make_plan(seg_num, seg_len, k);
+  return radix_topk_amd::run(plan, d_input, nullptr, seg_num, seg_len, seg_len, k, d_output_values,
+                             d_output_indices, d_workspace, workspace_bytes, stream);
+}
+
+size_t radix_topk_batch_topk_half_segmented_workspace_size(int seg_num, int max_seg_len, int k) {
+  if (seg_num <= 0 || max_seg_len < 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return 0;
+  const radix_topk_amd::Plan plan = make_plan(seg_num, max_seg_len, k);
+  return plan.ok ? plan.ws_bytes : 0;
+}
+
+int radix_topk_batch_topk_half_segmented(const uint16_t* d_input, const int32_t* d_offsets,
+                                         int seg_num, int max_seg_len, int k,
+                                         uint16_t* d_output_values, int32_t* d_output_indices,
+                                         void* d_workspace, size_t workspace_bytes,
+                                         void* stream) {
+  if (seg_num <= 0 || max_seg_len < 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return kInvalid;
+  if (!d_input || !d_offsets || !d_output_values || !d_output_indices || !d_workspace) return kInvalid;
+  const radix_topk_amd::Plan plan = make_plan(seg_num, max_seg_len, k);
+  return radix_topk_amd::run(plan, d_input, d_offsets, seg_num, 0, max_seg_len, k, d_output_values,
+                             d_output_indices, d_workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

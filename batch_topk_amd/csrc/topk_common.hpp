@@ -1,0 +1,58 @@
+// Shared host/device definitions of the batched fp16 top-k engine.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace radix_topk_amd {
+
+// Kernel parameter block of the fused segmented top-k kernel.  Every segment s covers the
+// element range [s0, s1) of `base` (a 16-byte aligned pointer); s0/s1 come from the int32
+// offsets when given, else from s * seg_len.  `elem0` is the element offset of the caller's
+// input pointer from `base` (0..7), added to every segment bound.
+struct TopkParams {
+  const uint16_t* base;
+  const int32_t* offsets;       // device [seg_num + 1] or nullptr (fixed-length segments)
+  int64_t elem0;
+  int64_t seg_len;              // fixed-length mode only
+  int64_t max_len;              // longest segment the launch covers; longer rows are padded
+  int32_t seg_num;
+  int32_t k;
+  int32_t chunks_per_seg;       // W: workgroups per segment; grid.x = seg_num * W
+  int32_t cap_chunk;            // LDS capacity of one chunk's candidate list
+  int32_t cap_list;             // workspace capacity of one chunk's published list
+  int32_t cand_area;            // LDS entries of the candidate / merge area
+  int32_t kpad;                 // LDS entries of the selection area (power of two >= k)
+  int32_t pad_;
+  uint16_t* out_vals;           // [seg_num, k]
+  int32_t* out_idx;             // [seg_num, k]
+  unsigned long long* tickets;  // [seg_num] arrival words (epoch << 16 | count)
+  int32_t* list_counts;         // [seg_num * W]
+  unsigned long long* lists;    // [seg_num * W * cap_list] packed (key16 << 32 | index)
+  unsigned long long epoch;     // 48-bit token unique to this call
+};
+
+// One compiled instantiation of the fused kernel.
+struct KernelShape {
+  int block;  // threads per workgroup (multiple of 64)
+  int vpt;    // 16-byte vectors per thread
+};
+
+// Launch plan: everything the host derives from (seg_num, max segment length, k).
+struct Plan {
+  KernelShape shape;
+  int chunk;        // elements per workgroup = block * vpt * 8
+  int W;            // workgroups per segment
+  int cap_chunk;
+  int cap_list;
+  int cand_area;
+  int kpad;
+  size_t lds_bytes;
+  size_t ws_bytes;  // workspace bytes (includes 256 bytes of alignment slack)
+  bool ok;
+};
+
+// Device launch of the fused kernel for `plan` (implemented in topk_kernels.hip).
+int launch_segmented_topk(const Plan& plan, const TopkParams& params, void* stream);
+
+}  // namespace radix_topk_amd

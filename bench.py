@@ -1,0 +1,210 @@
+"""Benchmark of the batched fp16 top-k engine on one MI355X.
+
+Default workload: LLM-sampling logits, 128 segments x 128,256 fp16 (N(0, sd 2), 0.1 % of each
+row boosted by +8), k = 50.  One step = one call of radix_topk_batch_topk_half over the whole
+batch (the inputs already resident in HBM).  The input is replicated over >= 512 MB of
+distinct buffers and the timed calls rotate through them, so the 256 MB Infinity Cache cannot
+serve the reads; a cache-resident ("warm") timing of a single buffer is reported separately.
+
+Prints ONE JSON line (rank 0):
+  value       = whole-job segments per second over the timed steps;
+  roofline    = algorithmic bytes per launch / median kernel time from HIP events on the
+                launch stream, against the 8 TB/s HBM peak;
+  cpu_baseline= the reference's host verifier (std::stable_sort per segment, restated in
+                oracle/) timed on this host's cores over the whole batch.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--k K]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_BPS = 8.0e12
+METRIC = "segments/s and achieved HBM GB/s, fp16 top-50 over 128×128256 segments"
+
+
+def log(msg: str) -> None:
+    sys.stderr.write(f"[bench] {msg}\n")
+    sys.stderr.flush()
+
+
+def make_input(name: str):
+    from batch_topk_amd import workloads as wl
+
+    if name == "llm_logits":
+        bits = wl.llm_logits()
+        return bits, dict(workload="llm_logits: 128x128256 fp16 N(0,sd 2), 0.1% of each row +8",
+                          seg_num=128, seg_len=128256)
+    if name == "uniform_small":
+        bits = wl.uniform_small()
+        return bits, dict(workload="uniform_small: 16x4096 fp16 U(-1,1)", seg_num=16, seg_len=4096)
+    if name == "ties_special":
+        bits = wl.ties_special()
+        return bits, dict(workload="ties_special: 256x32000 fp16, 256 distinct values, 1% -inf, 0.1% NaN",
+                          seg_num=256, seg_len=32000)
+    raise SystemExit(f"unknown workload {name}")
+
+
+def cpu_baseline(bits: np.ndarray, k: int, threads: int):
+    """Reference host verifier over the whole batch, serial (threads=1) and threaded."""
+    from oracle import oracle as O  # the checker, timed as the CPU baseline only
+
+    seg_num, seg_len = bits.shape
+    t1, _ = O.time_batch_topk_half(bits, k, seg_num, seg_len=seg_len, threads=1, variant=0, reps=3)
+    tn, _ = O.time_batch_topk_half(bits, k, seg_num, seg_len=seg_len, threads=threads, variant=0, reps=3)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(value=seg_num / t1, unit="segments/s", cores=1, kind="port",
+                sample=f"all {seg_num} segments x {seg_len} (the full batch), std::stable_sort per "
+                       f"segment as cpu_reference_topk, median of 3 runs",
+                threaded=dict(value=seg_num / tn, unit="segments/s", cores=threads),
+                cpu_model=cpu_model)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="llm_logits")
+    ap.add_argument("--k", type=int, default=50)
+    ap.add_argument("--rotate-mb", type=int, default=512)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the engine has no "
+              f"multi-GPU path", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import batch_topk_amd as bt
+
+    bt.load_library()
+    dev = torch.device("cuda:0")
+    bits, cfg = make_input(args.workload)
+    seg_num, seg_len = bits.shape
+    k = args.k
+    in_bytes = bits.nbytes
+    copies = max(1, -(-args.rotate_mb * 2**20 // in_bytes))
+    log(f"workload {cfg['workload']} k={k}, {copies} input copies ({copies * in_bytes / 2**20:.0f} MB)")
+    src = torch.from_numpy(bits.view(np.int16)).to(dev)
+    inputs = [src] + [src.clone() for _ in range(copies - 1)]
+    ws_bytes = bt.batch_topk_half_workspace_size(seg_num, seg_len, k)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    vals = torch.empty((seg_num, k), dtype=torch.int16, device=dev)
+    idx = torch.empty((seg_num, k), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+
+    def call(i: int) -> None:
+        rc = bt.batch_topk_half(inputs[i % copies].data_ptr(), seg_num, seg_len, k, vals.data_ptr(),
+                                idx.data_ptr(), ws.data_ptr(), ws_bytes, sh)
+        if rc != 0:
+            raise RuntimeError(f"batch_topk_half returned {rc}")
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+
+    # Parity spot check of the measured configuration (first segments, oracle as checker).
+    from oracle import oracle as O
+
+    call(0)
+    torch.cuda.synchronize()
+    ev, ei = O.batch_topk_half(bits[:8], k, seg_len=seg_len)
+    gi = idx.cpu().numpy()[:8]
+    gv = vals.cpu().numpy().view(np.uint16)[:8]
+    parity_ok = bool(np.array_equal(gi, ei) and np.array_equal(gv, ev))
+    log(f"parity spot check (8 segments vs oracle): {'ok' if parity_ok else 'MISMATCH'}")
+
+    # Timed region: K back-to-back steps, events on the launch stream.
+    steps = args.steps
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(steps):
+        call(i)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(stop)
+    ms_per_step = total_ms / steps
+
+    # Per-launch durations (events bracketing each launch), cold (rotating) and warm.
+    def per_launch(n: int, rotate: bool):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * n)]
+        torch.cuda.synchronize()
+        for i in range(n):
+            evs[2 * i].record(stream)
+            call(i if rotate else 0)
+            evs[2 * i + 1].record(stream)
+        torch.cuda.synchronize()
+        return np.array([evs[2 * i].elapsed_time(evs[2 * i + 1]) for i in range(n)]) * 1e3  # us
+
+    cold_us = per_launch(max(50, min(steps, 400)), True)
+    warm_us = per_launch(100, False)
+    kern_us = float(np.median(cold_us))
+
+    alg_bytes = 2 * seg_num * seg_len + 6 * seg_num * k
+    achieved = alg_bytes / (kern_us * 1e-6)
+    value = seg_num * steps / (total_ms * 1e-3)
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "segments/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u16",
+        "data": "synthetic",
+        "config": dict(cfg, k=k, input_copies=copies, parallelism="single GPU"),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved / 1e9,
+            "peak": HBM_PEAK_BPS / 1e9,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_BPS,
+            "traffic": None,
+        },
+        "elements_per_s": seg_num * seg_len * steps / (total_ms * 1e-3),
+        "hbm_gbps_whole_job": alg_bytes * steps / (total_ms * 1e-3) / 1e9,
+        "kernel_us_median": kern_us,
+        "kernel_us_p10_p90": [float(np.percentile(cold_us, 10)), float(np.percentile(cold_us, 90))],
+        "warm_kernel_us_median": float(np.median(warm_us)),
+        "alg_bytes_per_launch": alg_bytes,
+        "parity_spot_check": parity_ok,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (reference host verifier)...")
+        t0 = time.time()
+        result["cpu_baseline"] = cpu_baseline(bits, k, args.cpu_threads)
+        log(f"cpu baseline done in {time.time() - t0:.1f} s")
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result))
+    sys.stdout.flush()
+    return 0 if parity_ok else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,90 @@
+/*
+ * batch_topk for AMD Instinct MI355X (gfx950) -- C ABI.
+ *
+ * Batched fp16 top-k with int32 index output.  For every segment the k best values are
+ * returned in descending order together with their segment-local indices.  The order
+ * is total and deterministic: larger value first, equal values by ascending index, every
+ * NaN (any sign or payload) below -inf, and +0 equal to -0.  Output values are the raw
+ * 16-bit patterns read from the input at the selected index (NaN payloads and the sign
+ * of zero are preserved).
+ *
+ * All pointers named d_* are device pointers (hipMalloc'd or equivalent).  fp16 data
+ * travels as uint16_t bit patterns so that plain C and FFI callers need no half type;
+ * the memory layout is identical to __half.  `stream` is a hipStream_t (NULL = the
+ * null stream).  Every call is stream-ordered and asynchronous; nothing is allocated
+ * and the host never synchronises.
+ *
+ * Return values are hipError_t codes as int: 0 = hipSuccess; 1 = hipErrorInvalidValue
+ * for any rejected argument, returned before any HIP call is made; otherwise the HIP
+ * error of the failed launch.
+ *
+ * The workspace is owned by the caller, its content on entry may be arbitrary, and it
+ * must not be shared by calls that can run concurrently.
+ */
+#ifndef BATCH_TOPK_AMD_BATCH_TOPK_H_
+#define BATCH_TOPK_AMD_BATCH_TOPK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Largest k accepted by every entry point. */
+#define RADIX_TOPK_MAX_K 1024
+
+/*
+ * Fixed-length segments: segment s is d_input[s*seg_len, (s+1)*seg_len).
+ * Outputs are [seg_num, k] row-major.
+ *
+ * Replaces radix_topk::batch_topk_half (reference include/batch_topk.cuh:10-19,
+ * implemented at src/batch_topk.cu:42-193) with the same argument order and meaning.
+ * Rejected (-> 1): seg_num <= 0, seg_len <= 0, k <= 0, k > seg_len, k > RADIX_TOPK_MAX_K,
+ * any NULL pointer, workspace_bytes below the size reported by
+ * radix_topk_batch_topk_half_workspace_size (reference src/batch_topk.cu:13-33).
+ */
+int radix_topk_batch_topk_half(const uint16_t* d_input, int seg_num, int seg_len, int k,
+                               uint16_t* d_output_values, int32_t* d_output_indices,
+                               void* d_workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes for radix_topk_batch_topk_half; 0 for an unsupported shape.
+ * Replaces radix_topk::batch_topk_half_workspace_size (reference include/batch_topk.cuh:21,
+ * src/batch_topk.cu:35-40).  Depends only on the shape (and on the device's CU count,
+ * which is queried once), never on the data.
+ */
+size_t radix_topk_batch_topk_half_workspace_size(int seg_num, int seg_len, int k);
+
+/*
+ * Variable-length segments: segment s is d_input[d_offsets[s], d_offsets[s+1]),
+ * d_offsets being a device int32 array of seg_num + 1 non-decreasing entries.
+ * max_seg_len is a host-known upper bound on every segment length and sizes the launch.
+ * Segments shorter than k (including empty ones) fill ranks >= length with index -1 and
+ * value bits 0xFFFF.  A segment longer than max_seg_len breaks the precondition: its
+ * whole output row is filled with that pad.
+ *
+ * No counterpart in the reference, which has fixed-length segments only; it extends
+ * radix_topk::batch_topk_half (reference include/batch_topk.cuh:10-19) with the offset
+ * array used by segmented callers.
+ * Rejected (-> 1): seg_num <= 0, max_seg_len < 0, k <= 0, k > RADIX_TOPK_MAX_K, any NULL
+ * pointer, workspace_bytes below radix_topk_batch_topk_half_segmented_workspace_size.
+ */
+int radix_topk_batch_topk_half_segmented(const uint16_t* d_input, const int32_t* d_offsets,
+                                         int seg_num, int max_seg_len, int k,
+                                         uint16_t* d_output_values, int32_t* d_output_indices,
+                                         void* d_workspace, size_t workspace_bytes,
+                                         void* stream);
+
+/*
+ * Workspace bytes for radix_topk_batch_topk_half_segmented; 0 for an unsupported shape.
+ * Extends radix_topk::batch_topk_half_workspace_size (reference include/batch_topk.cuh:21)
+ * to the segmented entry point.
+ */
+size_t radix_topk_batch_topk_half_segmented_workspace_size(int seg_num, int max_seg_len, int k);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* BATCH_TOPK_AMD_BATCH_TOPK_H_ */

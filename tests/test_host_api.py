@@ -1,0 +1,115 @@
+"""Host-side checks of the C ABI that need no GPU: the library loads, exports every symbol
+include/batch_topk.h declares, validates arguments before any HIP call (reference
+src/batch_topk.cu:13-33 and test/test_batch_topk.cu:1168-1174,1311-1373), and sizes the
+workspace from the shape alone (src/batch_topk.cu:35-40)."""
+
+import os
+import re
+import subprocess
+
+import pytest
+
+import batch_topk_amd as bt
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INVALID = bt.HIP_ERROR_INVALID_VALUE
+# Dummy, never-dereferenced device addresses: every call below is rejected before use.
+P_IN, P_VAL, P_IDX, P_WS, P_OFF = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+
+
+def declared_symbols():
+    with open(os.path.join(ROOT, "include", "batch_topk.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(radix_topk_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = bt.load_library()
+    decl = declared_symbols()
+    assert decl == sorted(bt.EXPORTED_SYMBOLS)
+    for name in decl:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", bt.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(line.split()[-1] for line in out.splitlines() if " T " in line)
+    assert set(decl) <= exported
+
+
+def test_cpp_dropin_header_forwards_to_c_abi(tmp_path):
+    # The C++ drop-in (include/batch_topk.hpp) compiles against HIP headers and adds no symbols.
+    src = tmp_path / "use.cpp"
+    src.write_text('#include "batch_topk.hpp"\n'
+                   'size_t f(int a, int b, int c) { return radix_topk::batch_topk_half_workspace_size(a, b, c); }\n'
+                   'hipError_t g(const __half* x, __half* v, int* i, void* w, size_t n, hipStream_t s) {\n'
+                   '  return radix_topk::batch_topk_half(x, 1, 8, 3, v, i, w, n, s); }\n')
+    res = subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"),
+                          "-I", "/opt/rocm/include", "-c", str(src), "-o", str(tmp_path / "use.o")],
+                         capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+
+
+def test_workspace_size_contract():
+    # invalid shapes -> 0 (test/test_batch_topk.cu:1168-1174 keeps (0,10000,50) and (1,10,11))
+    assert bt.batch_topk_half_workspace_size(0, 10000, 50) == 0
+    assert bt.batch_topk_half_workspace_size(1, 10, 11) == 0
+    assert bt.batch_topk_half_workspace_size(1, 10000, 0) == 0
+    assert bt.batch_topk_half_workspace_size(1, 0, 1) == 0
+    assert bt.batch_topk_half_workspace_size(1, 2000, bt.MAX_K + 1) == 0
+    # lifted envelope: the reference's seg_len <= 10000 and k <= 128 limits are gone
+    assert bt.batch_topk_half_workspace_size(1, 10001, 50) > 1
+    assert bt.batch_topk_half_workspace_size(1, 10000, 129) > 1
+    assert bt.batch_topk_half_workspace_size(128, 128256, 50) > 1
+    assert bt.batch_topk_half_workspace_size(256, 32000, 256) > 1
+    # > 1 so that "workspace_bytes - 1" is a meaningful short workspace (test:1311-1314)
+    ws = bt.batch_topk_half_workspace_size(1, 10000, 50)
+    assert ws > 1
+    # far below the legacy per-element Candidate storage (test:270-280)
+    assert bt.batch_topk_half_workspace_size(128, 10000, 50) < 128 * 10000 * 12
+    # shape-only: repeated queries agree
+    assert ws == bt.batch_topk_half_workspace_size(1, 10000, 50)
+    # segmented variant
+    assert bt.batch_topk_half_segmented_workspace_size(512, 65536, 64) > 1
+    assert bt.batch_topk_half_segmented_workspace_size(0, 65536, 64) == 0
+    assert bt.batch_topk_half_segmented_workspace_size(4, -1, 64) == 0
+    assert bt.batch_topk_half_segmented_workspace_size(4, 100, 0) == 0
+
+
+def test_validation_rejects_before_any_hip_call():
+    ws = bt.batch_topk_half_workspace_size(1, 10000, 50)
+    call = bt.batch_topk_half
+    # null pointers (test/test_batch_topk.cu:1340-1373)
+    assert call(0, 1, 10000, 50, P_VAL, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, 1, 10000, 50, 0, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, 1, 10000, 50, P_VAL, 0, P_WS, ws) == INVALID
+    assert call(P_IN, 1, 10000, 50, P_VAL, P_IDX, 0, ws) == INVALID
+    # k > seg_len, bad sizes
+    assert call(P_IN, 1, 10, 11, P_VAL, P_IDX, P_WS, 1 << 20) == INVALID
+    assert call(P_IN, 0, 10, 1, P_VAL, P_IDX, P_WS, 1 << 20) == INVALID
+    assert call(P_IN, 1, 0, 1, P_VAL, P_IDX, P_WS, 1 << 20) == INVALID
+    assert call(P_IN, 1, 10, 0, P_VAL, P_IDX, P_WS, 1 << 20) == INVALID
+    assert call(P_IN, 1, 5000, bt.MAX_K + 1, P_VAL, P_IDX, P_WS, 1 << 30) == INVALID
+    # short workspace (test/test_batch_topk.cu:1375-1385)
+    assert call(P_IN, 1, 10000, 50, P_VAL, P_IDX, P_WS, ws - 1) == INVALID
+    # misaligned element pointers
+    assert call(P_IN + 1, 1, 10000, 50, P_VAL, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, 1, 10000, 50, P_VAL + 1, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, 1, 10000, 50, P_VAL, P_IDX + 2, P_WS, ws) == INVALID
+
+
+def test_segmented_validation_rejects_before_any_hip_call():
+    ws = bt.batch_topk_half_segmented_workspace_size(4, 1000, 64)
+    call = bt.batch_topk_half_segmented
+    assert call(0, P_OFF, 4, 1000, 64, P_VAL, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, 0, 4, 1000, 64, P_VAL, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, P_OFF, 0, 1000, 64, P_VAL, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, P_OFF, 4, -1, 64, P_VAL, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, P_OFF, 4, 1000, 0, P_VAL, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, P_OFF, 4, 1000, 64, P_VAL, P_IDX, P_WS, ws - 1) == INVALID
+    assert call(P_IN, P_OFF + 2, 4, 1000, 64, P_VAL, P_IDX, P_WS, ws) == INVALID
+
+
+def test_torch_helpers_fail_loudly_without_gpu():
+    torch = pytest.importorskip("torch")
+    x = torch.zeros((2, 8), dtype=torch.float16)
+    with pytest.raises(ValueError):
+        bt.topk(x, 3)   # CPU tensor: there is no CPU fallback

@@ -1,0 +1,199 @@
+"""GPU parity: the HIP engine, called through the C ABI, against the oracle and the reference
+tests' known answers.  Bit-exact on indices and on the raw fp16 bits of every value."""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import batch_topk_amd as bt
+from batch_topk_amd import workloads as wl
+from oracle import oracle as O
+from tests.gpu_util import announce, assert_properties, assert_same, run_fixed, run_segmented
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "kats.json")
+THREADS = 8
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    bt.load_library()
+
+
+def oracle_fixed(bits, k):
+    return O.batch_topk_half(bits, k, seg_len=bits.shape[1], threads=THREADS)
+
+
+def check_fixed(bits, k, what, **kw):
+    announce(f"{what} shape={bits.shape} k={k} {kw}")
+    got = run_fixed(bits, k, **kw)
+    assert_same(got, oracle_fixed(bits, k), what)
+    return got
+
+
+# ------------------------------------------------------------------ reference known answers
+
+def test_golden_cases():
+    with open(GOLDEN) as f:
+        cases = json.load(f)["cases"]
+    for c in cases:
+        bits = np.array(c["input_bits"], dtype=np.uint16).reshape(c["seg_num"], c["seg_len"])
+        poison = 0xA5 if "poisoned" in c["name"] else None
+        announce(f"golden {c['name']}")
+        vals, idx = run_fixed(bits, c["k"], poison=poison)
+        assert idx.tolist() == c["expected_idx"], c["name"]
+        assert vals.tolist() == c["expected_val_bits"], c["name"]
+
+
+@pytest.mark.parametrize("seg_num,seg_len,k,seed", [
+    (1, 10000, 50, 7), (8, 10000, 50, 17), (32, 10000, 50, 23),   # test:596-600
+    (3, 256, 128, 2026),                                           # test:817-920
+    (128, 10000, 50, 1234),                                        # test:1028-1141
+])
+def test_reference_random_cases(seg_num, seg_len, k, seed):
+    _, bits = O.make_random_input(seg_num, seg_len, seed)
+    check_fixed(bits.reshape(seg_num, seg_len), k, f"reference random seed={seed}")
+
+
+def test_reference_smoke_all_zero_row():
+    # test/test_batch_topk.cu:1319-1385: a zero row of 10000, k = 50 -> indices 0..49.
+    bits = np.zeros((1, 10000), dtype=np.uint16)
+    vals, idx = check_fixed(bits, 50, "all-zero row")
+    assert idx[0].tolist() == list(range(50))
+
+
+# ------------------------------------------------------------------ the five workloads
+
+def test_uniform_small():
+    check_fixed(wl.uniform_small(), 50, "uniform_small 16x4096")
+
+
+def test_llm_logits_full():
+    bits = wl.llm_logits()
+    vals, idx = check_fixed(bits, 50, "llm_logits 128x128256")
+    assert_properties(bits, vals, idx, 50, [bits.shape[1]] * bits.shape[0])
+
+
+def test_varlen_segments():
+    bits, offsets = wl.varlen()
+    announce("varlen 512 segments k=64")
+    got = run_segmented(bits, offsets, 64, 65536, poison=0xA5)
+    exp = O.batch_topk_half(bits, 64, offsets=offsets.astype(np.int64), threads=THREADS)
+    assert_same(got, exp, "varlen")
+    lengths = np.diff(offsets)
+    assert np.all(got[1][lengths == 1, 1:] == bt.PAD_INDEX)
+
+
+@pytest.mark.parametrize("k", [1, 16, 128, 256])
+def test_ties_special(k):
+    bits = wl.ties_special()
+    check_fixed(bits, k, "ties_special 256x32000")
+
+
+def test_huge_segment():
+    if bt.batch_topk_half_workspace_size(1, 16_777_216, 1024) == 0:
+        pytest.skip("single-segment path for 16,777,216 elements with k = 1024 not built yet")
+    bits = wl.huge_segment()
+    check_fixed(bits, 1024, "huge_segment 1x16777216")
+
+
+# ------------------------------------------------------------------ edge cases
+
+def _edge_rows():
+    rng = np.random.default_rng(99)
+    rows = {}
+    rows["all_equal"] = np.full((3, 5000), 0x3C00, dtype=np.uint16)
+    rows["all_nan"] = np.tile(np.array([0x7E00, 0xFE00, 0x7C01, 0xFFFF], dtype=np.uint16), (2, 1250))
+    rows["all_neg_inf"] = np.full((2, 3000), 0xFC00, dtype=np.uint16)
+    rows["all_negative"] = (rng.integers(0x8001, 0xFBFF, size=(4, 7000))).astype(np.uint16)
+    rows["signed_zeros"] = rng.choice(np.array([0x0000, 0x8000], dtype=np.uint16), size=(2, 4000))
+    x = rng.integers(0, 65536, size=(4, 9001)).astype(np.uint16)
+    rows["random_bits"] = x
+    y = np.full((2, 6000), 0xBC00, dtype=np.uint16)
+    y[:, rng.integers(0, 6000, size=100)] = 0x7E00
+    rows["nan_sprinkled_negatives"] = y
+    z = np.sort(rng.standard_normal((2, 20000)).astype(np.float16), axis=1).view(np.uint16)
+    rows["sorted_ascending"] = z
+    rows["sorted_descending"] = z[:, ::-1].copy()
+    d = (rng.integers(-3, 4, size=(2, 40000)) * 0.5).astype(np.float16).view(np.uint16)
+    rows["few_distinct_long"] = d
+    rows["subnormals"] = rng.integers(0x0001, 0x03FF, size=(2, 5000)).astype(np.uint16) | \
+        (rng.integers(0, 2, size=(2, 5000)).astype(np.uint16) << 15)
+    return rows
+
+
+@pytest.mark.parametrize("name", list(_edge_rows().keys()))
+@pytest.mark.parametrize("k", [1, 50, 300])
+def test_edge_rows(name, k):
+    bits = _edge_rows()[name]
+    if k > bits.shape[1]:
+        pytest.skip("k > seg_len")
+    vals, idx = check_fixed(bits, k, f"edge {name}")
+    assert_properties(bits, vals, idx, k, [bits.shape[1]] * bits.shape[0])
+
+
+@pytest.mark.parametrize("seg_len,k", [(1, 1), (7, 7), (8, 3), (63, 63), (64, 50), (65, 64),
+                                       (257, 256), (1000, 1000), (4096, 1024), (4097, 1)])
+def test_small_and_k_equal_len(seg_len, k):
+    rng = np.random.default_rng(seg_len * 31 + k)
+    bits = rng.standard_normal((5, seg_len)).astype(np.float16).view(np.uint16)
+    check_fixed(bits, k, f"small seg_len={seg_len}")
+
+
+@pytest.mark.parametrize("elem_offset", [1, 3, 7])
+@pytest.mark.parametrize("seg_len", [4099, 40001])
+def test_misaligned_input(elem_offset, seg_len):
+    rng = np.random.default_rng(elem_offset)
+    bits = rng.standard_normal((6, seg_len)).astype(np.float16).view(np.uint16)
+    check_fixed(bits, 50, "misaligned", elem_offset=elem_offset)
+
+
+def test_multichunk_ties_across_chunks():
+    # equal values spread across several workgroups of one segment: index order must hold
+    bits = np.full((4, 100_000), 0x3C00, dtype=np.uint16)
+    bits[:, ::997] = 0x4000
+    for k in (1, 50, 150, 700):
+        check_fixed(bits, k, "multichunk ties")
+
+
+def test_repeated_calls_share_workspace():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((16, 60000)).astype(np.float16).view(np.uint16)
+    ws = torch.empty(bt.batch_topk_half_workspace_size(16, 60000, 50), dtype=torch.uint8,
+                     device="cuda:0")
+    ws.fill_(0xA5)
+    for rep in range(3):
+        announce(f"repeated call {rep}")
+        got = run_fixed(a, 50, workspace=ws)
+        assert_same(got, oracle_fixed(a, 50), f"repeat {rep}")
+
+
+def test_varlen_edge_segments():
+    rng = np.random.default_rng(17)
+    lengths = np.array([0, 1, 2, 7, 8, 9, 63, 64, 65, 1000, 0, 65536, 33333, 5, 0], dtype=np.int64)
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    bits = rng.standard_normal(int(offsets[-1])).astype(np.float16).view(np.uint16)
+    for k, elem_offset in ((64, 0), (64, 3), (1, 5), (200, 0)):
+        announce(f"varlen edges k={k} offset={elem_offset}")
+        got = run_segmented(bits, offsets, k, 65536, elem_offset=elem_offset)
+        exp = O.batch_topk_half(bits, k, offsets=offsets.astype(np.int64), threads=THREADS)
+        assert_same(got, exp, f"varlen edges k={k}")
+
+
+def test_varlen_segment_longer_than_declared_max_is_padded():
+    rng = np.random.default_rng(2)
+    lengths = np.array([100, 5000, 100], dtype=np.int64)
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    bits = rng.standard_normal(int(offsets[-1])).astype(np.float16).view(np.uint16)
+    announce("varlen precondition violation")
+    vals, idx = run_segmented(bits, offsets, 10, 200)
+    exp = O.batch_topk_half(bits, 10, offsets=offsets.astype(np.int64))
+    assert np.array_equal(idx[0], exp[1][0]) and np.array_equal(idx[2], exp[1][2])
+    assert np.all(idx[1] == -1) and np.all(vals[1] == 0xFFFF)
