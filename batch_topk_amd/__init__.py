@@ -17,7 +17,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libbatch_topk_amd.so")
+# BATCH_TOPK_AMD_LIB selects another build of the same library (e.g. a tuning variant).
+LIB_PATH = os.environ.get("BATCH_TOPK_AMD_LIB") or os.path.join(_HERE, "libbatch_topk_amd.so")
 
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1

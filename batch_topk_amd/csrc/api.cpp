@@ -20,7 +20,6 @@ namespace radix_topk_amd {
 namespace {
 
 constexpr int kMaxK = RADIX_TOPK_MAX_K;
-constexpr int kMaxCandArea = 4096;  // LDS entries (8 B each) of the candidate / merge area
 constexpr size_t kAlign = 256;
 constexpr int kInvalid = static_cast<int>(hipErrorInvalidValue);
 
@@ -34,44 +33,51 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // Launch plan for segments of at most `max_len` elements (plus up to 7 elements of
 // misalignment of the 16-byte load grid), `seg_num` segments and `k` outputs each.
+//
+// A segment that fits one workgroup (<= kMaxChunk elements) gets exactly one, of the smallest
+// shape (vectors per thread first, then threads) that covers it, with at least 4k threads so
+// each wave's share of k stays well below its 64 lanes.  Longer segments are split into
+// kMaxChunk chunks whose candidate lists are merged by the last workgroup to finish.
 Plan make_plan(int seg_num, int64_t max_len, int k) {
   Plan plan{};
   plan.ok = false;
   if (seg_num <= 0 || k <= 0 || k > kMaxK || max_len < 0) return plan;
-  // Threads per workgroup grow with k so that each wave's share of k stays well below its
-  // 64 lanes (the threshold step picks the ceil(k / waves)-th best lane of every wave).
-  const int block = k <= 64 ? 256 : (k <= 128 ? 512 : 1024);
+  const int block_min = k <= 64 ? 256 : (k <= 128 ? 512 : 1024);
   const int64_t span = max_len + 7;  // worst-case aligned span of one segment
-  int vpt = 8;
-  for (int cand : {2, 4, 8}) {
-    if (static_cast<int64_t>(block) * cand * 8 >= span) {
-      vpt = cand;
-      break;
+  int block = 1024, vpt = 16;
+  bool found = false;
+  for (int cv : {2, 4, 8, 16}) {
+    for (int cb = block_min; cb <= 1024 && !found; cb *= 2) {
+      if (static_cast<int64_t>(cb) * cv * 8 >= span) {
+        block = cb;
+        vpt = cv;
+        found = true;
+      }
     }
+    if (found) break;
   }
   const int chunk = block * vpt * 8;
   const int64_t W = span <= chunk ? 1 : (span + chunk - 1) / chunk;
   const int kpad = next_pow2(k < 64 ? 64 : k);
-  const int cap_chunk = 2 * kpad > 2048 ? 2 * kpad : 2048;
-  const int cap_list = W > 1 ? (2 * kpad > 256 ? 2 * kpad : 256) : 0;
-  const int64_t merge_area = W * static_cast<int64_t>(cap_list);
-  const int64_t cand_area = merge_area > cap_chunk ? merge_area : cap_chunk;
-  if (cand_area > kMaxCandArea) return plan;  // segment too long for the fused merge
+  const int cap_list = W > 1 ? next_pow2(2 * k > 128 ? 2 * k : 128) : 0;
+  if (W > 1 && W * static_cast<int64_t>(cap_list) > kCandArea) return plan;  // too long to merge
   if (static_cast<int64_t>(seg_num) * W > 0x7fffffff) return plan;
 
   plan.shape = KernelShape{block, vpt};
   plan.chunk = chunk;
   plan.W = static_cast<int>(W);
-  plan.cap_chunk = cap_chunk;
+  plan.cap_chunk = kCandArea;
   plan.cap_list = cap_list;
-  plan.cand_area = static_cast<int>(cand_area);
+  plan.cand_area = kCandArea;
   plan.kpad = kpad;
-  plan.lds_bytes = 256 * 4 + 16 * 4 + 16 * 4 + static_cast<size_t>(cand_area) * 8 +
-                   static_cast<size_t>(kpad) * 8 + static_cast<size_t>(kpad) * 4;
-  size_t ws = kAlign;                                   // alignment slack of the carve
+  const int rank_cap = kpad > 512 ? kpad : 512;
+  plan.lds_bytes = 256 * 4 + 256 * 4 + 32 * 4 + 16 * 4 + static_cast<size_t>(kCandArea) * 8 +
+                   static_cast<size_t>(kpad) * 8 + static_cast<size_t>(rank_cap) * 4 +
+                   static_cast<size_t>(block / 64) * kStageWords * 4;
+  size_t ws = kAlign;                                        // alignment slack of the carve
   ws += align_up(static_cast<size_t>(seg_num) * 8, kAlign);  // arrival tickets
   if (W > 1) {
-    ws += align_up(static_cast<size_t>(seg_num) * W * 4, kAlign);             // list counts
+    ws += align_up(static_cast<size_t>(seg_num) * W * 4, kAlign);               // list counts
     ws += static_cast<size_t>(seg_num) * W * static_cast<size_t>(cap_list) * 8;  // lists
   }
   plan.ws_bytes = ws;

@@ -6,6 +6,14 @@
 
 namespace radix_topk_amd {
 
+// LDS entries (8 bytes each) of a workgroup's candidate area: the per-wave candidate regions,
+// then the contiguous candidate list, and for a multi-workgroup segment the merged lists.
+constexpr int kCandArea = 2048;
+// Per-wave private LDS region of the filter, in 32-bit words (kStageWords / 2 candidates).
+constexpr int kStageWords = 512;
+// Longest chunk one workgroup covers: 1024 threads x 16 vectors x 8 elements.
+constexpr int kMaxChunk = 1024 * 16 * 8;
+
 // Kernel parameter block of the fused segmented top-k kernel.  Every segment s covers the
 // element range [s0, s1) of `base` (a 16-byte aligned pointer); s0/s1 come from the int32
 // offsets when given, else from s * seg_len.  `elem0` is the element offset of the caller's

@@ -1,31 +1,36 @@
 // Fused segmented fp16 top-k for gfx950 (MI355X).
 //
-// One workgroup owns one chunk (block * vpt * 8 elements) of one segment and reads it from
-// HBM exactly once, with 16-byte loads, into registers.  Everything after the load runs on
-// registers and LDS:
+// One workgroup owns one chunk (block * vpt * 8 elements) of one segment; a segment of up to
+// 131,072 elements is a single chunk.  The chunk is read from HBM exactly once, with
+// nontemporal 16-byte loads that are all issued up front, into registers.  Everything after
+// the load runs on registers and LDS, overlapped with the loads still in flight:
 //
-//   1. thread best     packed int16 max/min over the raw fp16 bits (v_pk_max_i16 /
-//                      v_pk_min_i16, one op per two elements).  The int16 max is the best
+//   1. thread best     over the first half of the vectors: packed int16 max/min trees over the
+//                      raw fp16 bits (v_pk_max_i16 / v_pk_min_i16).  The int16 max is the best
 //                      non-negative-sign element, the int16 min the best negative-sign one;
-//                      whichever applies is a real element of the thread (or, for a NaN,
-//                      a worse one), which is all the threshold step needs.
-//   2. threshold       each wave takes the ceil(kc / waves)-th smallest descending key of
-//                      its lanes' bests with a 16-step ballot radix select (no LDS, no
-//                      atomics); T = the largest of the wave results.  At least kc real
-//                      elements have key <= T, so every element of the chunk's top kc does.
-//   3. compaction      one pass over the registers with a single integer compare per
-//                      element; hits are appended to an LDS list (wave-aggregated atomic
-//                      slot) as packed (key16 << 32 | segment index).  If the list would
-//                      overflow (ties, all-equal rows), an exact 4-digit radix refinement
-//                      over (key16, position16) on the registers shrinks it first.
-//   4. selection       an LDS radix select over the packed 48-bit (key, index) values finds
-//                      the exact k-th entry, then a rank sort (or, for <= 64 entries, a
-//                      wave64 register bitonic) orders the survivors.
-//   5. output          values are re-read raw from the input at the selected index.
+//                      whichever applies is a real element of the thread (or, for a NaN, a
+//                      worse one), which is all the threshold needs.
+//   2. threshold       T = the kc-th smallest descending key among the thread bests, found
+//                      exactly with two LDS histogram passes (high byte, then low byte inside
+//                      the boundary bucket) and DPP prefix scans.  At least kc real elements
+//                      have key <= T, so every element of the chunk's top kc does.
+//   3. filter          only a lane whose best key is <= T can hold a candidate.  Each wave
+//                      copies those lanes' words into its LDS staging area and tests them one
+//                      word per lane, so the work follows the candidate lanes (a few per wave
+//                      on logits), not the chunk.  Hits reserve their LDS slots with one atomic
+//                      per wave and step and are written at ballot/mbcnt offsets, packed as
+//                      (key16 << 48 | index32 << 16 | raw16): one u64 compare orders
+//                      (key, index), and the raw bits ride along to the output.
+//                      If the list overflows (ties, all-equal rows), an exact radix refinement
+//                      over (key16, position17), re-reading the chunk, rebuilds it.
+//   4. selection       small sets: every wave holds the whole list in registers and ranks its
+//                      share by ballot counts; larger sets: LDS radix select over the packed
+//                      values down to exactly k, then rank counting.
+//   5. output          index and raw value bits of each selected candidate.
 //
-// Segments longer than one chunk are split over W workgroups.  Each publishes its list to
-// the workspace, and the last to arrive (an epoch-tagged arrival counter, so the workspace
-// needs no initialisation) merges the lists with step 4.
+// Segments longer than one chunk are split over W workgroups; each publishes its list to the
+// workspace and the last to arrive (an epoch-tagged arrival counter, so the workspace needs no
+// initialisation) merges the lists with step 4.
 //
 // Ordering contract (reference include/batch_topk_types.cuh:70-82,100-113 and
 // include/type_codec.cuh:9-38): ascending (desc_key, index), where desc_key maps every NaN
@@ -37,15 +42,29 @@
 
 #include "topk_common.hpp"
 
+// Phase timestamp hook for profiling builds; compiled out otherwise.
+#ifndef TOPK_TRACE
+#define TOPK_TRACE(id)
+#endif
+#ifndef TOPK_WTRACE
+#define TOPK_WTRACE(id)
+#endif
+#ifndef TOPK_TRACE_VALUE
+#define TOPK_TRACE_VALUE(id, value)
+#endif
+
 namespace radix_topk_amd {
 namespace {
 
 using u32 = uint32_t;
 using u64 = unsigned long long;
 typedef short short2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr u64 kMask48 = 0xFFFFFFFFFFFFull;
 constexpr u32 kFillWord = 0xFFFFFFFFu;  // two negative NaNs: never a candidate, never a best
+constexpr int kArea = kCandArea;        // LDS candidate entries (candidate list, merged lists)
+constexpr int kRankCap = 512;           // rank-counting path handles up to this many
 
 // ------------------------------------------------------------------------------ codec
 
@@ -59,6 +78,13 @@ __device__ __forceinline__ u32 desc_key(u32 b) {
   return key;
 }
 
+// Candidate packing: ascending u64 order == ascending (key, index); raw bits carried along.
+__device__ __forceinline__ u64 pack_candidate(u32 raw, u32 index) {
+  return (static_cast<u64>(desc_key(raw)) << 48) | (static_cast<u64>(index) << 16) | raw;
+}
+__device__ __forceinline__ u32 cand_index(u64 P) { return static_cast<u32>(P >> 16); }
+__device__ __forceinline__ u32 cand_raw(u64 P) { return static_cast<u32>(P) & 0xffffu; }
+
 // ------------------------------------------------------------------------------ wave64 helpers
 
 __device__ __forceinline__ u64 ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
@@ -68,10 +94,6 @@ __device__ __forceinline__ u32 mbcnt(u64 m) {
                                    __builtin_amdgcn_mbcnt_lo(static_cast<u32>(m), 0u));
 }
 
-__device__ __forceinline__ u32 shfl_u32(u32 x, int src_lane) {
-  return static_cast<u32>(__builtin_amdgcn_ds_bpermute(src_lane << 2, static_cast<int>(x)));
-}
-
 __device__ __forceinline__ u64 shfl_xor_u64(u64 x, int mask, int lane) {
   const int src = (lane ^ mask) << 2;
   const u32 lo = static_cast<u32>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(static_cast<u32>(x))));
@@ -79,33 +101,21 @@ __device__ __forceinline__ u64 shfl_xor_u64(u64 x, int mask, int lane) {
   return (static_cast<u64>(hi) << 32) | lo;
 }
 
-__device__ __forceinline__ u32 wave_inclusive_scan(u32 x, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const u32 y = shfl_u32(x, lane >= d ? lane - d : lane);
-    if (lane >= d) x += y;
-  }
-  return x;
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ u32 dpp(u32 x) {
+  return static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROW_MASK, 0xf, false));
 }
 
-// kth (1-based, wave-uniform, 1..64) smallest 16-bit key across the 64 lanes of a wave:
-// MSB-first binary radix select with ballots.  Pure SALU bookkeeping per bit.
-__device__ __forceinline__ u32 wave_kth_smallest16(u32 key, int kth) {
-  u64 run = ~0ull;
-  u32 prefix = 0;
-#pragma unroll
-  for (int bit = 15; bit >= 0; --bit) {
-    const u64 zeros = ballot(((key >> bit) & 1u) == 0u) & run;
-    const int cz = __popcll(zeros);
-    if (kth <= cz) {
-      run = zeros;
-    } else {
-      kth -= cz;
-      run &= ~zeros;
-      prefix |= 1u << bit;
-    }
-  }
-  return prefix;
+// Inclusive prefix sum across a wave64 with DPP: row_shr 1/2/4/8 inside each 16-lane row,
+// then row_bcast:15 and row_bcast:31 carry the row totals upward.
+__device__ __forceinline__ u32 wave_inclusive_scan(u32 x) {
+  x += dpp<0x111, 0xf>(x);
+  x += dpp<0x112, 0xf>(x);
+  x += dpp<0x114, 0xf>(x);
+  x += dpp<0x118, 0xf>(x);
+  x += dpp<0x142, 0xa>(x);
+  x += dpp<0x143, 0xc>(x);
+  return x;
 }
 
 // Ascending bitonic sort of one u64 per lane across a wave64.
@@ -129,35 +139,38 @@ __device__ __forceinline__ u64 wave_bitonic_sort64(u64 x, int lane) {
 
 struct Smem {
   u32* hist;    // [256]
-  int* scal;    // [16]
-  u32* wave_t;  // [16]
-  u64* cand;    // [cand_area]
+  u32* hist2;   // [256]
+  int* scal;    // [32]
+  u32* wcnt;    // [16] (spare)
+  u64* area;    // [kArea] contiguous candidate list
   u64* sel;     // [kpad]
-  int* rank;    // [kpad]
+  int* rank;    // [max(kpad, kRankCap)]
+  u32* stage;   // [NW][kStageWords] per-wave filter regions
 };
 
-__device__ __forceinline__ Smem carve_smem(unsigned char* smem, int cand_area, int kpad) {
+__device__ __forceinline__ Smem carve_smem(unsigned char* smem, int kpad) {
   Smem s;
   s.hist = reinterpret_cast<u32*>(smem);
-  s.scal = reinterpret_cast<int*>(s.hist + 256);
-  s.wave_t = reinterpret_cast<u32*>(s.scal + 16);
-  s.cand = reinterpret_cast<u64*>(s.wave_t + 16);
-  s.sel = s.cand + cand_area;
+  s.hist2 = s.hist + 256;
+  s.scal = reinterpret_cast<int*>(s.hist2 + 256);
+  s.wcnt = reinterpret_cast<u32*>(s.scal + 32);
+  s.area = reinterpret_cast<u64*>(s.wcnt + 16);
+  s.sel = s.area + kArea;
   s.rank = reinterpret_cast<int*>(s.sel + kpad);
+  s.stage = reinterpret_cast<u32*>(s.rank + (kpad > kRankCap ? kpad : kRankCap));
   return s;
 }
 
 // Wave 0: find the histogram bucket holding the need-th (1-based) entry.  Writes
-// scal[0] = bucket, scal[1] = entries in earlier buckets, scal[2] = entries in the bucket.
-__device__ __forceinline__ void wave_find_bucket(const u32* hist, int need, int* scal, int lane) {
+// out[0] = bucket, out[1] = entries in earlier buckets, out[2] = entries in the bucket.
+__device__ __forceinline__ void wave_find_bucket(const u32* hist, int need, int* out, int lane) {
   const u32 c0 = hist[lane * 4 + 0], c1 = hist[lane * 4 + 1];
   const u32 c2 = hist[lane * 4 + 2], c3 = hist[lane * 4 + 3];
   const u32 sum = c0 + c1 + c2 + c3;
-  const u32 incl = wave_inclusive_scan(sum, lane);
+  const u32 incl = wave_inclusive_scan(sum);
   const u32 excl = incl - sum;
   const u32 uneed = static_cast<u32>(need);
-  const bool mine = excl < uneed && uneed <= incl;
-  if (mine) {
+  if (excl < uneed && uneed <= incl) {
     u32 run = excl;
     int b = lane * 4;
     u32 cnt = c0;
@@ -176,15 +189,15 @@ __device__ __forceinline__ void wave_find_bucket(const u32* hist, int need, int*
         }
       }
     }
-    scal[0] = b;
-    scal[1] = static_cast<int>(run);
-    scal[2] = static_cast<int>(cnt);
+    out[0] = b;
+    out[1] = static_cast<int>(run);
+    out[2] = static_cast<int>(cnt);
   }
 }
 
-// Exact radix select over M unique packed 48-bit values in LDS: returns the bound B such
-// that exactly kk values are <= B (1 <= kk <= M).  8-bit digits, MSB first, early exit as
-// soon as a bucket is taken whole.
+// Exact radix select over M unique packed values in LDS: returns the bound B such that
+// exactly kk values are <= B (1 <= kk <= M).  8-bit digits over the key and index fields,
+// MSB first, early exit as soon as a bucket is taken whole.
 template <int BLOCK>
 __device__ u64 block_select_bound(const u64* list, int M, int kk, u32* hist, int* scal) {
   const int tid = threadIdx.x;
@@ -192,7 +205,7 @@ __device__ u64 block_select_bound(const u64* list, int M, int kk, u32* hist, int
   const int wid = tid >> 6;
   u64 prefix = 0, pmask = 0;
   int need = kk;
-  for (int shift = 40; shift >= 0; shift -= 8) {
+  for (int shift = 56; shift >= 16; shift -= 8) {
     for (int i = tid; i < 256; i += BLOCK) hist[i] = 0;
     __syncthreads();
     for (int i = tid; i < M; i += BLOCK) {
@@ -210,30 +223,93 @@ __device__ u64 block_select_bound(const u64* list, int M, int kk, u32* hist, int
     pmask |= 0xffull << shift;
     if (need == cnt) break;
   }
-  return prefix | (~pmask & kMask48);
+  return prefix | ~pmask;
 }
 
-// Writes rank r of segment output: index + raw value re-read from the input.  An entry
-// outside the segment (only a padding sentinel can be) is written as the pad.
-__device__ __forceinline__ void write_rank(const TopkParams& p, int64_t s0, int64_t n, int seg,
-                                           int r, u64 P) {
-  const u32 idx = static_cast<u32>(P);
+// Writes rank r of the segment's output row.  An entry outside the segment (only a padding
+// sentinel can be) is written as the pad.
+__device__ __forceinline__ void write_rank(const TopkParams& p, int64_t n, int seg, int r, u64 P) {
+  const u32 idx = cand_index(P);
   const int64_t o = static_cast<int64_t>(seg) * p.k + r;
   if (r >= p.k) return;
   if (static_cast<int64_t>(idx) < n) {
     p.out_idx[o] = static_cast<int>(idx);
-    p.out_vals[o] = p.base[s0 + idx];
+    p.out_vals[o] = static_cast<uint16_t>(cand_raw(P));
   } else {
     p.out_idx[o] = -1;
     p.out_vals[o] = 0xffffu;
   }
 }
 
-// Select the kk best of the M packed candidates in LDS (M >= kk) and write them, in order,
-// to the segment's output row; ranks kk..k-1 get the pad (index -1, bits 0xFFFF).
+// rank[i] = #{j : v[j] < v[i]} over the M entries of v, comparisons split over all threads.
 template <int BLOCK>
-__device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int kk, int64_t s0,
-                                 int64_t n, int seg) {
+__device__ void block_rank(const u64* v, int M, int* rank) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < M; i += BLOCK) rank[i] = 0;
+  __syncthreads();
+  const int slices = BLOCK / M > 0 ? BLOCK / M : 1;
+  const int span = (M + slices - 1) / slices;
+  for (int t = tid; t < M * slices; t += BLOCK) {
+    const int i = t % M;
+    const int q = t / M;
+    const int j0 = q * span;
+    const int j1 = j0 + span < M ? j0 + span : M;
+    const u64 P = v[i];
+    int c = 0;
+    for (int j = j0; j < j1; ++j) c += v[j] < P ? 1 : 0;
+    if (slices == 1) {
+      rank[i] = c;
+    } else if (c) {
+      atomicAdd(&rank[i], c);
+    }
+  }
+  __syncthreads();
+}
+
+// Ranks the M (<= 64 * S) unique candidates of `list` and stores those of rank < kk at
+// sel[rank].  Every wave holds the whole list in registers (S u64 per lane) and ranks its
+// share of the candidates with ballots: rank(x) = sum over slots of popcount(ballot(c < x)).
+template <int BLOCK, int S>
+__device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
+                                int kk) {
+  constexpr int NW = BLOCK / 64;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  u64 c[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int i = s * 64 + lane;
+    c[s] = i < M ? list[i] : ~0ull;
+  }
+  const int slots = (M + 63) >> 6;
+  // This wave's candidates are i = wid + NW * t; lane t fetches the t-th one, so all of them
+  // come from LDS in one round, and each is then broadcast with a lane read.  Its rank (the
+  // number of smaller entries) lands back in lane t, which writes the output row directly.
+  constexpr int PER = 64 * S / NW;  // upper bound of candidates per wave (M <= 64 * S)
+  static_assert(PER <= 64, "one candidate per lane");
+  const int mine_i = wid + NW * lane;
+  const u64 mine = (lane < PER && mine_i < M) ? list[mine_i] : ~0ull;
+  const int count = M > wid ? (M - wid + NW - 1) / NW : 0;
+  int my_rank = kk;
+  for (int t = 0; t < count; ++t) {
+    const u32 xl = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(mine)), t));
+    const u32 xh = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(mine >> 32)), t));
+    const u64 x = (static_cast<u64>(xh) << 32) | xl;
+    int r = 0;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (s < slots) r += __popcll(ballot(c[s] < x));
+    }
+    my_rank = lane == t ? r : my_rank;
+  }
+  if (lane < count && my_rank < kk) write_rank(p, n, seg, my_rank, mine);
+}
+
+// Select the kk best of the M packed candidates in `sm.area` (M >= kk) and write them, in
+// order, to the segment's output row; ranks kk..k-1 get the pad (index -1, bits 0xFFFF).
+template <int BLOCK>
+__device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int kk, int64_t n,
+                                 int seg) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = tid >> 6;
@@ -243,54 +319,49 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
     p.out_idx[o] = -1;
     p.out_vals[o] = 0xffffu;
   }
-  if (M <= 64) {
-    if (wid == 0) {
-      u64 x = lane < M ? sm.cand[lane] : ~0ull;
-      x = wave_bitonic_sort64(x, lane);
-      if (lane < kk) write_rank(p, s0, n, seg, lane, x);
-    }
+  constexpr int NW = BLOCK / 64;
+  // Small sets: every wave ranks its share against the whole list held in registers and
+  // writes the output entries of its candidates that rank below kk.
+  if (M <= 128) {
+    wave_rank_write<BLOCK, 2>(p, n, seg, sm.area, M, kk);
     return;
   }
-  const u64* sel = sm.cand;
+  if constexpr (NW >= 8) {
+    if (M <= 8 * NW * 4 && M <= 512) {
+      wave_rank_write<BLOCK, 8>(p, n, seg, sm.area, M, kk);
+      return;
+    }
+  }
+  const u64* sel = sm.area;
   if (M > kk) {
-    const u64 bound = block_select_bound<BLOCK>(sm.cand, M, kk, sm.hist, sm.scal);
+    const u64 bound = block_select_bound<BLOCK>(sm.area, M, kk, sm.hist, sm.scal);
     if (tid == 0) sm.scal[3] = 0;
     __syncthreads();
     for (int i = tid; i < M; i += BLOCK) {
-      const u64 P = sm.cand[i];
+      const u64 P = sm.area[i];
       if (P <= bound) {
         const int slot = atomicAdd(&sm.scal[3], 1);
         if (slot < p.kpad) sm.sel[slot] = P;
       }
     }
+    __syncthreads();
     sel = sm.sel;
   }
-  for (int i = tid; i < kk; i += BLOCK) sm.rank[i] = 0;
-  __syncthreads();
-  // Rank sort: rank(i) = #{j : sel[j] < sel[i]}; the comparisons are split over all threads.
-  const int slices = BLOCK / kk > 0 ? BLOCK / kk : 1;
-  const int span = (kk + slices - 1) / slices;
-  for (int t = tid; t < kk * slices; t += BLOCK) {
-    const int i = t % kk;
-    const int q = t / kk;
-    const int j0 = q * span;
-    const int j1 = j0 + span < kk ? j0 + span : kk;
-    const u64 P = sel[i];
-    int c = 0;
-    for (int j = j0; j < j1; ++j) c += sel[j] < P ? 1 : 0;
-    if (slices == 1) {
-      sm.rank[i] = c;
-    } else if (c) {
-      atomicAdd(&sm.rank[i], c);
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < kk; i += BLOCK) write_rank(p, s0, n, seg, sm.rank[i], sel[i]);
+  block_rank<BLOCK>(sel, kk, sm.rank);
+  for (int i = tid; i < kk; i += BLOCK) write_rank(p, n, seg, sm.rank[i], sel[i]);
 }
 
 // Epoch-tagged arrival counter: word = epoch << 16 | count.  A word carrying another epoch
 // is stale (earlier call, or uninitialised workspace) and counts as zero.  The last
 // arriver resets the count to zero, so a replay with the same epoch also works.
+//
+// Cross-workgroup publication protocol.  Every word one workgroup writes for another
+// (list entries, list counts, this ticket) is an agent-scope atomic, which gfx950 lowers to
+// device-coherent (sc1) vector memory accesses.  The writer waits for its stores to complete
+// (s_waitcnt vmcnt(0)) before its arrival CAS, and the merger only issues its sc1 loads after
+// its own CAS returned.  That is the agent-scope release/acquire pair restricted to sc1
+// accesses, without the whole-L2 writeback (buffer_wbl2) and invalidate (buffer_inv) the
+// generic fences add for plain stores and loads.
 __device__ __forceinline__ bool arrive_last(u64* ticket, u64 epoch, int arrivals) {
   u64 old = __hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (;;) {
@@ -298,11 +369,33 @@ __device__ __forceinline__ bool arrive_last(u64* ticket, u64 epoch, int arrivals
     const u64 next = cnt + 1u;
     const bool last = next >= static_cast<u64>(arrivals);
     const u64 word = (epoch << 16) | (last ? 0u : next);
-    if (__hip_atomic_compare_exchange_strong(ticket, &old, word, __ATOMIC_ACQ_REL,
+    if (__hip_atomic_compare_exchange_strong(ticket, &old, word, __ATOMIC_RELAXED,
                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
       return last;
     }
   }
+}
+
+__device__ __forceinline__ void wait_vector_memory() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Nontemporal 16-byte load at a 32-bit byte offset from a wave-uniform base (so the
+// address stays in the scalar base + 32-bit vector offset form).
+__device__ __forceinline__ uint4 load_nt(const unsigned char* base, u32 byte_off) {
+  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + byte_off));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+
+__device__ __forceinline__ short2_t as_s2(u32 w) { return __builtin_bit_cast(short2_t, w); }
+__device__ __forceinline__ u32 as_u32(short2_t w) { return __builtin_bit_cast(u32, w); }
+
+// Packed int16 max / min of the 8 halves of a vector, as the two halves of one word.
+__device__ __forceinline__ u32 vec_max2(const uint4& x) {
+  return as_u32(__builtin_elementwise_max(__builtin_elementwise_max(as_s2(x.x), as_s2(x.y)),
+                                          __builtin_elementwise_max(as_s2(x.z), as_s2(x.w))));
+}
+__device__ __forceinline__ u32 vec_min2(const uint4& x) {
+  return as_u32(__builtin_elementwise_min(__builtin_elementwise_min(as_s2(x.x), as_s2(x.y)),
+                                          __builtin_elementwise_min(as_s2(x.z), as_s2(x.w))));
 }
 
 // ------------------------------------------------------------------------------ the kernel
@@ -311,10 +404,13 @@ template <int BLOCK, int VPT>
 __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   constexpr int NW = BLOCK / 64;
   constexpr int CH = BLOCK * VPT * 8;
-  static_assert(CH <= 65536, "chunk positions are packed into 16 bits");
+  constexpr int JT = VPT;  // vectors the threshold is computed from
+  static_assert(CH <= 65536 * 2, "chunk positions must fit the refinement packing");
+  static_assert(NW <= 16, "at most 16 waves");
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const Smem sm = carve_smem(smem_raw, p.cand_area, p.kpad);
+  const Smem sm = carve_smem(smem_raw, p.kpad);
 
+  TOPK_TRACE(0);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = tid >> 6;
@@ -364,95 +460,175 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   const int hi = static_cast<int>(c1 - cb);
   const u32 idx_base = static_cast<u32>(cb - s0);  // segment index = idx_base + position
 
-  // ---- 1. load the chunk (one HBM read, 16-byte vectors, coalesced per wave)
+  // ---- 1. load the chunk: all nontemporal 16-byte loads issued before any is consumed; a
+  // block with no element of the chunk re-reads the chunk's first block (always in bounds).
   uint4 v[VPT];
-  const uint16_t* cptr = p.base + cb;
+  const unsigned char* cptr = reinterpret_cast<const unsigned char*>(p.base + cb);
+  const u32 lo_blk = static_cast<u32>(lo & ~7);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int pos = (j * BLOCK + tid) * 8;
-    if (pos < hi && pos + 8 > lo) {
-      v[j] = *reinterpret_cast<const uint4*>(cptr + pos);
-      if (pos < lo || pos + 8 > hi) {
-        u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    const bool any = pos < hi && pos + 8 > lo;
+    v[j] = load_nt(cptr, (any ? static_cast<u32>(pos) : lo_blk) * 2u);
+  }
+  for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
+  __syncthreads();  // histogram cleared (the loads stay in flight)
+  TOPK_TRACE(12);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (pos + e < lo || pos + e >= hi) w4[e >> 1] |= 0xffffu << ((e & 1) * 16);
-        }
-        v[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  for (int j = 0; j < VPT; ++j) {
+    const int pos = (j * BLOCK + tid) * 8;
+    if (pos < lo || pos + 8 > hi) {  // edge or empty block: fill outside [lo, hi)
+      u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (pos + e < lo || pos + e >= hi) w4[e >> 1] |= 0xffffu << ((e & 1) * 16);
       }
-    } else {
-      v[j] = make_uint4(kFillWord, kFillWord, kFillWord, kFillWord);
+      v[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
     }
   }
 
-  // ---- 2. thread best (packed int16 max / min over raw bits)
+  // ---- 2. thread best over the first JT vectors (packed int16 max / min trees)
+  u32 gmax[JT];  // per-vector packed int16 max, kept for the filter's vector test
   short2_t mx = {static_cast<short>(-32768), static_cast<short>(-32768)};
   short2_t mn = {32767, 32767};
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const short2_t x = __builtin_bit_cast(short2_t, w4[q]);
-      mx = __builtin_elementwise_max(mx, x);
-      mn = __builtin_elementwise_min(mn, x);
-    }
+  for (int j = 0; j < JT; ++j) {
+    gmax[j] = vec_max2(v[j]);
+    mx = __builtin_elementwise_max(mx, as_s2(gmax[j]));
+    mn = __builtin_elementwise_min(mn, as_s2(vec_min2(v[j])));
   }
-  const int m1 = mx.x > mx.y ? mx.x : mx.y;
+  const int m1 = mx.x > mx.y ? mx.x : mx.y;  // int16 max: the best non-negative-sign half
   const int m2 = mn.x < mn.y ? mn.x : mn.y;
   const u32 best_key = desc_key(static_cast<u32>(m1 >= 0 ? m1 : m2) & 0xffffu);
+  TOPK_TRACE(1);
 
-  // ---- 3. threshold T: at least kc real elements of the chunk have key <= T
-  const int kw = (kc + NW - 1) / NW;
-  if (tid == 0) sm.scal[4] = 0;
-  if (kw <= 64) {
-    const u32 tw = wave_kth_smallest16(best_key, kw);
-    if (lane == 0) sm.wave_t[wid] = tw;
-  }
+  // ---- 3. threshold T = kc-th smallest thread best, by two histogram passes
+  atomicAdd(&sm.hist[best_key >> 8], 1u);
+  if (tid < 256) sm.hist2[tid] = 0;
+  if (tid == 0) sm.scal[4] = 0;  // candidate list counter
   __syncthreads();
-  u32 T = 0xffffu;
-  if (kw <= 64) {
-    T = 0;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) T = sm.wave_t[i] > T ? sm.wave_t[i] : T;
+  if (wid == 0) wave_find_bucket(sm.hist, kc, sm.scal + 8, lane);
+  __syncthreads();
+  TOPK_TRACE(2);
+  const u32 b1 = static_cast<u32>(sm.scal[8]);
+  u32 T;
+  if (sm.scal[9] + sm.scal[10] <= kc + 64 && b1 < 0xffu) {
+    // Few thread bests up to the boundary bucket: its upper end is threshold enough (the
+    // filter then keeps every element of the bucket; the selection sorts them out).
+    T = (b1 << 8) | 0xffu;
+  } else {
+    if ((best_key >> 8) == b1) atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
+    __syncthreads();
+    if (wid == 0) wave_find_bucket(sm.hist2, kc - sm.scal[9], sm.scal + 12, lane);
+    __syncthreads();
+    T = (b1 << 8) | static_cast<u32>(sm.scal[12]);
   }
+  TOPK_TRACE(4);
+  TOPK_WTRACE(0);
 
-  // ---- 4. compaction of {key <= T} into the LDS list
-  const int cap = p.cap_chunk;
-  auto emit = [&](bool hit, u32 b, int pos) {
-    const u64 m = ballot(hit);
-    if (m) {
-      const int leader = __ffsll(static_cast<long long>(m)) - 1;
-      int base = 0;
-      if (lane == leader) base = atomicAdd(&sm.scal[4], __popcll(m));
-      base = static_cast<int>(shfl_u32(static_cast<u32>(base), leader));
+  // ---- 4. filter {key <= T} into the contiguous LDS candidate list.  Each wave first collects
+  // its hits in a private LDS region (ballot/mbcnt slots, no atomics), then reserves its
+  // share of the list with one LDS atomic and copies the region there.  LDS instructions are
+  // serialised per CU, so the filter issues one only where a ballot found hits.
+  // Candidates are packed as (key16 << 48 | index32 << 16 | raw16).
+  const bool all_mode = T == 0xffffu;  // no usable threshold: fewer than kc bests, or NaNs
+  if (!all_mode) {
+    constexpr int RC = kStageWords / 2;  // region capacity (u64 entries) per wave
+    u64* region = reinterpret_cast<u64*>(sm.stage + wid * kStageWords);
+    u32 wcount = 0;  // wave-uniform
+    auto put = [&](bool hit, u64 m, u64 P) {
       if (hit) {
-        const int slot = base + static_cast<int>(mbcnt(m));
-        if (slot < cap) sm.cand[slot] = (static_cast<u64>(desc_key(b)) << 32) | (idx_base + static_cast<u32>(pos));
+        const u32 slot = wcount + mbcnt(m);
+        if (slot < static_cast<u32>(RC)) region[slot] = P;
+      }
+      wcount += static_cast<u32>(__popcll(m));
+    };
+    if (T < 0x7fffu) {
+      // T is a positive value: candidates are the b in [raw(T), 0x7C00] (positive, non-NaN).
+      // A vector can hold one only if the int16 max of its halves is >= raw(T): two compares
+      // on the packed max (the low half as int16, the high half as the whole word against
+      // raw(T) << 16).  Inside such a vector, one packed subtract d = b - raw(T) per word and
+      // two unsigned compares (low half, whole word) give the exact hits: d <= 0x7C00 - raw(T)
+      // holds exactly for raw(T) <= b <= 0x7C00.
+      const u32 t_lo = T ^ 0x7fffu;
+      const int t_hi = static_cast<int>(t_lo) << 16;
+      const ushort2_t tt = {static_cast<unsigned short>(t_lo), static_cast<unsigned short>(t_lo)};
+      const u32 span = 0x7c00u - t_lo;
+      const u32 span_hi = (span << 16) | 0xffffu;
+      u64 vhit[VPT];
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const u32 g = gmax[j];
+        vhit[j] = ballot(static_cast<short>(g) >= static_cast<int>(t_lo) || static_cast<int>(g) >= t_hi);
+      }
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        if (vhit[j]) {
+          const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+          const u32 pos0 = static_cast<u32>((j * BLOCK + tid) * 8) + idx_base;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const u32 d = __builtin_bit_cast(u32, __builtin_bit_cast(ushort2_t, w4[q]) - tt);
+            const bool h_lo = static_cast<unsigned short>(d) <= span;
+            const bool h_hi = d <= span_hi;
+            const u64 m_lo = ballot(h_lo);
+            const u64 m_hi = ballot(h_hi);
+            if (m_lo) {
+              const u32 b = w4[q] & 0xffffu, pi = pos0 + 2u * q;
+              put(h_lo, m_lo, (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b));
+            }
+            if (m_hi) {
+              const u32 b = w4[q] >> 16, pi = pos0 + 2u * q + 1u;
+              put(h_hi, m_hi, (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b));
+            }
+          }
+        }
+      }
+    } else {
+      // T is +-0 or negative: candidates are every non-NaN positive and the b with
+      // uint16(b) <= raw(T) (raw of the zero class taken as 0x8000).
+      const u32 traw = T == 0x7fffu ? 0x8000u : T;
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+          const bool h = b <= traw && (b & 0x7fffu) <= 0x7c00u;
+          const u64 m = ballot(h);
+          if (m) put(h, m, pack_candidate(b, idx_base + static_cast<u32>((j * BLOCK + tid) * 8 + e)));
+        }
       }
     }
-  };
+    TOPK_WTRACE(1);
+    // Publish: one atomic reserves the wave's slots; a region that overflowed forces the
+    // exact refinement by pushing the count past kArea.
+    const u32 amount = wcount > static_cast<u32>(RC) ? static_cast<u32>(kArea) + 1u : wcount;
+    if (amount) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      u32 base = 0;
+      if (lane == 0) base = atomicAdd(reinterpret_cast<u32*>(&sm.scal[4]), amount);
+      base = __builtin_amdgcn_readfirstlane(base);
+      TOPK_WTRACE(2);
+      if (wcount <= static_cast<u32>(RC)) {
+        for (u32 i = lane; i < wcount; i += 64) {
+          if (base + i < static_cast<u32>(kArea)) sm.area[base + i] = region[i];
+        }
+      }
+      TOPK_WTRACE(3);
+    }
+  }
+  TOPK_TRACE(5);
+  TOPK_WTRACE(4);
+  __syncthreads();
+  TOPK_WTRACE(5);
 
-  if (T != 0xffffu) {
-    // Integer test on the raw bits equivalent to desc_key(b) <= T for non-NaN b:
-    //   T positive (key < 0x7FFF): int16(b) >= int16(raw(T));
-    //   T zero or negative:        uint16(b) <= raw(T)  (raw(+-0 class) taken as 0x8000).
-    const bool pos_t = T < 0x7fffu;
-    const u32 traw = pos_t ? (T ^ 0x7fffu) : (T == 0x7fffu ? 0x8000u : T);
-    const int traw_s = static_cast<int>(static_cast<short>(traw));
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        const bool pass = pos_t ? (static_cast<int>(static_cast<short>(b)) >= traw_s) : (b <= traw);
-        const bool hit = pass && (b & 0x7fffu) <= 0x7c00u;
-        emit(hit, b, (j * BLOCK + tid) * 8 + e);
-      }
-    }
-  } else if (nc <= cap) {
-    // No usable threshold (few elements per wave, or NaN-dominated rows): take the chunk.
+  int C = all_mode ? 0 : sm.scal[4];
+  const bool overflow = C > kArea;
+  if (all_mode && nc <= kArea) {
+    // Every in-range element, at its position: no counting needed.
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
@@ -460,36 +636,41 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
       for (int e = 0; e < 8; ++e) {
         const int pos = (j * BLOCK + tid) * 8 + e;
         const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        emit(pos >= lo && pos < hi, b, pos);
+        if (pos >= lo && pos < hi) sm.area[pos - lo] = pack_candidate(b, idx_base + static_cast<u32>(pos));
       }
     }
-  } else if (tid == 0) {
-    sm.scal[4] = nc;
-  }
-  __syncthreads();
-  int C = sm.scal[4];
-
-  if (C > cap) {
-    // ---- 4b. exact refinement on the registers: radix select over P = key16 << 16 | pos16
-    // among in-range elements with key <= T, until at most `cap` values are <= the bound.
-    u32 prefix = 0, pmask = 0;
-    int need = kc;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
-      __syncthreads();
-#pragma unroll
+    C = nc;
+    __syncthreads();
+  } else if (all_mode || overflow) {
+    // ---- 4b. exact refinement (rare: ties or NaN-dominated rows overflow the LDS list).
+    // Radix select over P = key16 << 17 | position17 among in-range elements with key <= T,
+    // until at most kArea values are <= the bound.  The chunk is re-read from memory for each
+    // pass, so the registers of the fast path are not kept live for it.
+    auto for_each_element = [&](auto&& fn) {
+#pragma unroll 1
       for (int j = 0; j < VPT; ++j) {
-        const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        const int pos0 = (j * BLOCK + tid) * 8;
+        if (pos0 < hi && pos0 + 8 > lo) {
+          const uint4 x = *reinterpret_cast<const uint4*>(cptr + static_cast<u32>(pos0) * 2u);
+          const u32 w4[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int pos = (j * BLOCK + tid) * 8 + e;
-          const u32 key = desc_key((w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
-          const u32 P = (key << 16) | static_cast<u32>(pos);
-          if (pos >= lo && pos < hi && key <= T && (P & pmask) == prefix) {
-            atomicAdd(&sm.hist[(P >> shift) & 255u], 1u);
+          for (int e = 0; e < 8; ++e) {
+            const int pos = pos0 + e;
+            if (pos >= lo && pos < hi) fn((w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu, pos);
           }
         }
       }
+    };
+    u64 prefix = 0, pmask = 0;
+    int need = kc;
+    for (int shift = 32; shift >= 0; shift -= 8) {
+      for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
+      __syncthreads();
+      for_each_element([&](u32 b, int pos) {
+        const u32 key = desc_key(b);
+        const u64 P = (static_cast<u64>(key) << 17) | static_cast<u32>(pos);
+        if (key <= T && (P & pmask) == prefix) atomicAdd(&sm.hist[(P >> shift) & 255u], 1u);
+      });
       __syncthreads();
       if (wid == 0) wave_find_bucket(sm.hist, need, sm.scal, lane);
       __syncthreads();
@@ -497,45 +678,46 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
       const int before = sm.scal[1];
       const int cnt = sm.scal[2];
       need -= before;
-      prefix |= static_cast<u32>(b) << shift;
-      pmask |= 0xffu << shift;
+      prefix |= static_cast<u64>(b) << shift;
+      pmask |= 0xffull << shift;
       const int count_le = (kc - need) + cnt;
-      if (count_le <= cap) break;
+      if (count_le <= kArea) break;
     }
-    const u32 bound = prefix | ~pmask;
+    const u64 bound = prefix | (~pmask & 0x1FFFFFFFFull);
     if (tid == 0) sm.scal[4] = 0;
     __syncthreads();
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int pos = (j * BLOCK + tid) * 8 + e;
-        const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        const u32 key = desc_key(b);
-        const u32 P = (key << 16) | static_cast<u32>(pos);
-        emit(pos >= lo && pos < hi && key <= T && P <= bound, b, pos);
+    for_each_element([&](u32 b, int pos) {
+      const u32 key = desc_key(b);
+      const u64 P = (static_cast<u64>(key) << 17) | static_cast<u32>(pos);
+      if (key <= T && P <= bound) {
+        const int slot = atomicAdd(&sm.scal[4], 1);
+        if (slot < kArea) sm.area[slot] = pack_candidate(b, idx_base + static_cast<u32>(pos));
       }
-    }
+    });
     __syncthreads();
     C = sm.scal[4];
+    C = C < kArea ? C : kArea;
   }
+  TOPK_TRACE(6);
+  TOPK_TRACE_VALUE(14, C);
+  TOPK_TRACE_VALUE(15, T);
 
   // ---- 5. single-chunk segment: select and write
   if (Ws == 1) {
-    finalize_segment<BLOCK>(p, sm, C, kk, s0, n, seg);
+    finalize_segment<BLOCK>(p, sm, C, kk, n, seg);
+    TOPK_TRACE(7);
     return;
   }
 
   // ---- 6. multi-chunk segment: publish this chunk's list, last arriver merges
-  const u64* src = sm.cand;
+  const u64* src = sm.area;
   int M = C;
   if (C > p.cap_list) {
-    const u64 bound = block_select_bound<BLOCK>(sm.cand, C, kc, sm.hist, sm.scal);
+    const u64 bound = block_select_bound<BLOCK>(sm.area, C, kc, sm.hist, sm.scal);
     if (tid == 0) sm.scal[3] = 0;
     __syncthreads();
     for (int i = tid; i < C; i += BLOCK) {
-      const u64 P = sm.cand[i];
+      const u64 P = sm.area[i];
       if (P <= bound) {
         const int slot = atomicAdd(&sm.scal[3], 1);
         if (slot < p.kpad) sm.sel[slot] = P;
@@ -547,26 +729,34 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   }
   const int64_t list_id = static_cast<int64_t>(seg) * W + w;
   u64* my_list = p.lists + list_id * p.cap_list;
-  for (int i = tid; i < M; i += BLOCK) my_list[i] = src[i];
-  if (tid == 0) p.list_counts[list_id] = M;
-  __threadfence();
+  for (int i = tid; i < M; i += BLOCK) {
+    __hip_atomic_store(my_list + i, src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (tid == 0) __hip_atomic_store(p.list_counts + list_id, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_vector_memory();
   __syncthreads();
+  TOPK_TRACE(8);
   if (tid == 0) sm.scal[5] = arrive_last(p.tickets + seg, p.epoch, Ws) ? 1 : 0;
   __syncthreads();
+  TOPK_TRACE(9);
   if (!sm.scal[5]) return;
-  __threadfence();
 
   int total = 0;
   for (int c = 0; c < Ws; ++c) {
     const int64_t id = static_cast<int64_t>(seg) * W + c;
     int cnt = __hip_atomic_load(p.list_counts + id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     cnt = cnt < 0 ? 0 : (cnt > p.cap_list ? p.cap_list : cnt);
+    if (total + cnt > kArea) cnt = kArea - total;
     const u64* lst = p.lists + id * p.cap_list;
-    for (int i = tid; i < cnt; i += BLOCK) sm.cand[total + i] = lst[i];
+    for (int i = tid; i < cnt; i += BLOCK) {
+      sm.area[total + i] = __hip_atomic_load(lst + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     total += cnt;
   }
   __syncthreads();
-  finalize_segment<BLOCK>(p, sm, total, kk, s0, n, seg);
+  TOPK_TRACE(10);
+  finalize_segment<BLOCK>(p, sm, total, kk, n, seg);
+  TOPK_TRACE(11);
 }
 
 template <int BLOCK, int VPT>
@@ -586,12 +776,15 @@ int launch_segmented_topk(const Plan& plan, const TopkParams& params, void* stre
   if (b == 256 && vpt == 2) return launch_shape<256, 2>(plan, params, s);
   if (b == 256 && vpt == 4) return launch_shape<256, 4>(plan, params, s);
   if (b == 256 && vpt == 8) return launch_shape<256, 8>(plan, params, s);
+  if (b == 256 && vpt == 16) return launch_shape<256, 16>(plan, params, s);
   if (b == 512 && vpt == 2) return launch_shape<512, 2>(plan, params, s);
   if (b == 512 && vpt == 4) return launch_shape<512, 4>(plan, params, s);
   if (b == 512 && vpt == 8) return launch_shape<512, 8>(plan, params, s);
+  if (b == 512 && vpt == 16) return launch_shape<512, 16>(plan, params, s);
   if (b == 1024 && vpt == 2) return launch_shape<1024, 2>(plan, params, s);
   if (b == 1024 && vpt == 4) return launch_shape<1024, 4>(plan, params, s);
   if (b == 1024 && vpt == 8) return launch_shape<1024, 8>(plan, params, s);
+  if (b == 1024 && vpt == 16) return launch_shape<1024, 16>(plan, params, s);
   return static_cast<int>(hipErrorInvalidValue);
 }
 
