@@ -61,6 +61,10 @@ using u64 = unsigned long long;
 typedef short short2_t __attribute__((ext_vector_type(2)));
 typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+// 32 words held in registers and read at a wave-uniform index (s_set_gpr_idx), so a loop over
+// a data-dependent set of a lane's vectors compiles to one short body instead of one per vector.
+typedef unsigned u32x32_t __attribute__((ext_vector_type(32)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr u32 kFillWord = 0xFFFFFFFFu;  // two negative NaNs: never a candidate, never a best
 constexpr int kArea = kCandArea;        // LDS candidate entries (candidate list, merged lists)
@@ -104,6 +108,17 @@ __device__ __forceinline__ u64 shfl_xor_u64(u64 x, int mask, int lane) {
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ u32 dpp(u32 x) {
   return static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROW_MASK, 0xf, false));
+}
+
+// OR of x over the wave (DPP OR-scan; lane 63 holds the total), returned wave-uniform.
+__device__ __forceinline__ u32 wave_or(u32 x) {
+  x |= dpp<0x111, 0xf>(x);
+  x |= dpp<0x112, 0xf>(x);
+  x |= dpp<0x114, 0xf>(x);
+  x |= dpp<0x118, 0xf>(x);
+  x |= dpp<0x142, 0xa>(x);
+  x |= dpp<0x143, 0xc>(x);
+  return static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(x), 63));
 }
 
 // Inclusive prefix sum across a wave64 with DPP: row_shr 1/2/4/8 inside each 16-lane row,
@@ -488,13 +503,14 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   }
 
   // ---- 2. thread best over the first JT vectors (packed int16 max / min trees)
-  u32 gmax[JT];  // per-vector packed int16 max, kept for the filter's vector test
+  i32x16_t gm;  // per-vector int16 max of the 8 halves, kept for the filter's vector test
   short2_t mx = {static_cast<short>(-32768), static_cast<short>(-32768)};
   short2_t mn = {32767, 32767};
 #pragma unroll
   for (int j = 0; j < JT; ++j) {
-    gmax[j] = vec_max2(v[j]);
-    mx = __builtin_elementwise_max(mx, as_s2(gmax[j]));
+    const short2_t g = as_s2(vec_max2(v[j]));
+    gm[j] = g.x > g.y ? g.x : g.y;
+    mx = __builtin_elementwise_max(mx, g);
     mn = __builtin_elementwise_min(mn, as_s2(vec_min2(v[j])));
   }
   const int m1 = mx.x > mx.y ? mx.x : mx.y;  // int16 max: the best non-negative-sign half
@@ -511,98 +527,142 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   __syncthreads();
   TOPK_TRACE(2);
   const u32 b1 = static_cast<u32>(sm.scal[8]);
-  u32 T;
-  if (sm.scal[9] + sm.scal[10] <= kc + 64 && b1 < 0xffu) {
-    // Few thread bests up to the boundary bucket: its upper end is threshold enough (the
-    // filter then keeps every element of the bucket; the selection sorts them out).
-    T = (b1 << 8) | 0xffu;
-  } else {
-    if ((best_key >> 8) == b1) atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
-    __syncthreads();
-    if (wid == 0) wave_find_bucket(sm.hist2, kc - sm.scal[9], sm.scal + 12, lane);
-    __syncthreads();
-    T = (b1 << 8) | static_cast<u32>(sm.scal[12]);
-  }
+  if ((best_key >> 8) == b1) atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
+  __syncthreads();
+  if (wid == 0) wave_find_bucket(sm.hist2, kc - sm.scal[9], sm.scal + 12, lane);
+  __syncthreads();
+  const u32 T = (b1 << 8) | static_cast<u32>(sm.scal[12]);
   TOPK_TRACE(4);
   TOPK_WTRACE(0);
 
-  // ---- 4. filter {key <= T} into the contiguous LDS candidate list.  Each wave first collects
-  // its hits in a private LDS region (ballot/mbcnt slots, no atomics), then reserves its
-  // share of the list with one LDS atomic and copies the region there.  LDS instructions are
-  // serialised per CU, so the filter issues one only where a ballot found hits.
-  // Candidates are packed as (key16 << 48 | index32 << 16 | raw16).
+  // ---- 4. filter {key <= T} into the contiguous LDS candidate list, packed as
+  // (key16 << 48 | index32 << 16 | raw16).  Scheduling matters more than work here: the
+  // waves' instruction streams are latency-bound and LDS instructions are serialised per CU.
   const bool all_mode = T == 0xffffu;  // no usable threshold: fewer than kc bests, or NaNs
-  if (!all_mode) {
-    constexpr int RC = kStageWords / 2;  // region capacity (u64 entries) per wave
-    u64* region = reinterpret_cast<u64*>(sm.stage + wid * kStageWords);
-    u32 wcount = 0;  // wave-uniform
-    auto put = [&](bool hit, u64 m, u64 P) {
-      if (hit) {
-        const u32 slot = wcount + mbcnt(m);
-        if (slot < static_cast<u32>(RC)) region[slot] = P;
+  if (!all_mode && T < 0x7fffu) {
+    // T is a positive value: candidates are the b in [raw(T), 0x7C00] (positive, non-NaN).
+    // A vector can hold one only if the int16 max of its halves is >= raw(T).  Each wave
+    // copies its lanes' vectors that pass this test into an LDS staging list (one 16-byte
+    // write per such vector), then tests the staged vectors one per lane: one packed
+    // subtract d = b - raw(T) per word and two unsigned compares give the exact hits
+    // (d <= 0x7C00 - raw(T) holds exactly for raw(T) <= b <= 0x7C00).  A wave prefix sum
+    // gives every hit its offset, and one LDS atomic per 64 staged vectors reserves the
+    // wave's slots in the list.
+    const u32 t_lo = T ^ 0x7fffu;
+    const ushort2_t tt = {static_cast<unsigned short>(t_lo), static_cast<unsigned short>(t_lo)};
+    const u32 span = 0x7c00u - t_lo;
+    const u32 span_hi = (span << 16) | 0xffffu;
+    uint4* st_vec = reinterpret_cast<uint4*>(sm.stage + wid * kStageWords);
+    u32* st_pos = sm.stage + wid * kStageWords + 256;
+    // Per-lane bit mask of the passing vectors (vector ALU only), OR-reduced over the wave.
+    u32 lane_bits = 0;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      lane_bits |= (static_cast<u32>(static_cast<int>(t_lo) - 1 - gm[j]) >> 31) << j;
+    }
+    const u32 hv = wave_or(lane_bits);
+    TOPK_WTRACE(2);
+    u32 nst = 0;  // staged vectors (wave-uniform)
+    auto flush = [&]() {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const bool valid = static_cast<u32>(lane) < nst;
+      const uint4 x = st_vec[lane];
+      const u32 p0 = idx_base + st_pos[lane];
+      const u32 w4[4] = {x.x, x.y, x.z, x.w};
+      bool h[8];
+      u32 cnt = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32 d = __builtin_bit_cast(u32, __builtin_bit_cast(ushort2_t, w4[q]) - tt);
+        h[2 * q] = valid && static_cast<unsigned short>(d) <= span;
+        h[2 * q + 1] = valid && d <= span_hi;
+        cnt += static_cast<u32>(h[2 * q]) + static_cast<u32>(h[2 * q + 1]);
       }
-      wcount += static_cast<u32>(__popcll(m));
-    };
-    if (T < 0x7fffu) {
-      // T is a positive value: candidates are the b in [raw(T), 0x7C00] (positive, non-NaN).
-      // A vector can hold one only if the int16 max of its halves is >= raw(T): two compares
-      // on the packed max (the low half as int16, the high half as the whole word against
-      // raw(T) << 16).  Inside such a vector, one packed subtract d = b - raw(T) per word and
-      // two unsigned compares (low half, whole word) give the exact hits: d <= 0x7C00 - raw(T)
-      // holds exactly for raw(T) <= b <= 0x7C00.
-      const u32 t_lo = T ^ 0x7fffu;
-      const int t_hi = static_cast<int>(t_lo) << 16;
-      const ushort2_t tt = {static_cast<unsigned short>(t_lo), static_cast<unsigned short>(t_lo)};
-      const u32 span = 0x7c00u - t_lo;
-      const u32 span_hi = (span << 16) | 0xffffu;
-      u64 vhit[VPT];
+      const u32 incl = wave_inclusive_scan(cnt);
+      const u32 total = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
+      if (total) {
+        u32 base = 0;
+        if (lane == 0) base = atomicAdd(reinterpret_cast<u32*>(&sm.scal[4]), total);
+        u32 o = __builtin_amdgcn_readfirstlane(base) + incl - cnt;
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        const u32 g = gmax[j];
-        vhit[j] = ballot(static_cast<short>(g) >= static_cast<int>(t_lo) || static_cast<int>(g) >= t_hi);
-      }
-#pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        if (vhit[j]) {
-          const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-          const u32 pos0 = static_cast<u32>((j * BLOCK + tid) * 8) + idx_base;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const u32 d = __builtin_bit_cast(u32, __builtin_bit_cast(ushort2_t, w4[q]) - tt);
-            const bool h_lo = static_cast<unsigned short>(d) <= span;
-            const bool h_hi = d <= span_hi;
-            const u64 m_lo = ballot(h_lo);
-            const u64 m_hi = ballot(h_hi);
-            if (m_lo) {
-              const u32 b = w4[q] & 0xffffu, pi = pos0 + 2u * q;
-              put(h_lo, m_lo, (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b));
-            }
-            if (m_hi) {
-              const u32 b = w4[q] >> 16, pi = pos0 + 2u * q + 1u;
-              put(h_hi, m_hi, (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b));
-            }
+        for (int e = 0; e < 8; ++e) {
+          if (h[e]) {
+            const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+            const u32 pi = p0 + static_cast<u32>(e);
+            if (o < static_cast<u32>(kArea))
+              sm.area[o] = (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b);
+            ++o;
           }
         }
       }
-    } else {
-      // T is +-0 or negative: candidates are every non-NaN positive and the b with
-      // uint16(b) <= raw(T) (raw of the zero class taken as 0x8000).
-      const u32 traw = T == 0x7fffu ? 0x8000u : T;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      nst = 0;
+    };
+    // Stage the passing vectors: a loop over the wave's passing vector indices, reading the
+    // vector at a uniform register index.
+    u32x32_t va, vb;
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    for (int j = 0; j < VPT; ++j) {
+      u32x32_t& dst = j < 8 ? va : vb;
+      const int b = (j & 7) * 4;
+      dst[b] = v[j].x;
+      dst[b + 1] = v[j].y;
+      dst[b + 2] = v[j].z;
+      dst[b + 3] = v[j].w;
+    }
+    auto stage = [&](const u32x32_t& a, u32 bits, int jbase) {
+      while (bits) {
+        const int jj = __builtin_ctz(bits);
+        bits &= bits - 1;
+        const bool mine = (lane_bits >> (jbase + jj)) & 1u;
+        const u64 m = ballot(mine);
+        const u32 c = static_cast<u32>(__popcll(m));
+        if (nst + c > 64u) flush();
+        if (mine) {
+          const u32 slot = nst + mbcnt(m);
+          st_vec[slot] = make_uint4(a[jj * 4], a[jj * 4 + 1], a[jj * 4 + 2], a[jj * 4 + 3]);
+          st_pos[slot] = static_cast<u32>(((jbase + jj) * BLOCK + tid) * 8);
+        }
+        nst += c;
+      }
+    };
+    stage(va, hv & 0xffu, 0);
+    if constexpr (VPT > 8) stage(vb, hv >> 8, 8);
+    TOPK_WTRACE(3);
+    if (nst) flush();
+    TOPK_WTRACE(4);
+  } else if (!all_mode) {
+    // T is +-0 or negative: candidates are every non-NaN positive and the b with
+    // uint16(b) <= raw(T) (raw of the zero class taken as 0x8000).  Each wave collects its hits
+    // in a private LDS region (ballot/mbcnt slots), then reserves its share of the list with
+    // one LDS atomic and copies the region there.
+    constexpr int RC = kStageWords / 2;  // region capacity (u64 entries) per wave
+    u64* region = reinterpret_cast<u64*>(sm.stage + wid * kStageWords);
+    u32 wcount = 0;  // wave-uniform
+    const u32 traw = T == 0x7fffu ? 0x8000u : T;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-          const bool h = b <= traw && (b & 0x7fffu) <= 0x7c00u;
-          const u64 m = ballot(h);
-          if (m) put(h, m, pack_candidate(b, idx_base + static_cast<u32>((j * BLOCK + tid) * 8 + e)));
+    for (int j = 0; j < VPT; ++j) {
+      const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+        const bool h = b <= traw && (b & 0x7fffu) <= 0x7c00u;
+        const u64 m = ballot(h);
+        if (m) {
+          if (h) {
+            const u32 slot = wcount + mbcnt(m);
+            if (slot < static_cast<u32>(RC))
+              region[slot] = pack_candidate(b, idx_base + static_cast<u32>((j * BLOCK + tid) * 8 + e));
+          }
+          wcount += static_cast<u32>(__popcll(m));
         }
       }
     }
-    TOPK_WTRACE(1);
-    // Publish: one atomic reserves the wave's slots; a region that overflowed forces the
-    // exact refinement by pushing the count past kArea.
+    // A region that overflowed forces the exact refinement by pushing the count past kArea.
     const u32 amount = wcount > static_cast<u32>(RC) ? static_cast<u32>(kArea) + 1u : wcount;
     if (amount) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -611,17 +671,14 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
       u32 base = 0;
       if (lane == 0) base = atomicAdd(reinterpret_cast<u32*>(&sm.scal[4]), amount);
       base = __builtin_amdgcn_readfirstlane(base);
-      TOPK_WTRACE(2);
       if (wcount <= static_cast<u32>(RC)) {
         for (u32 i = lane; i < wcount; i += 64) {
           if (base + i < static_cast<u32>(kArea)) sm.area[base + i] = region[i];
         }
       }
-      TOPK_WTRACE(3);
     }
   }
   TOPK_TRACE(5);
-  TOPK_WTRACE(4);
   __syncthreads();
   TOPK_WTRACE(5);
 
