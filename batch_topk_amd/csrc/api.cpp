@@ -37,7 +37,10 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // A segment that fits one workgroup (<= kMaxChunk elements) gets exactly one, of the smallest
 // shape (vectors per thread first, then threads) that covers it, with at least 4k threads so
 // each wave's share of k stays well below its 64 lanes.  Longer segments are split into
-// kMaxChunk chunks whose candidate lists are merged by the last workgroup to finish.
+// kMaxChunk chunks whose candidate lists are merged by the last workgroup to finish, while
+// the W lists fit one workgroup's LDS merge area.  Beyond that (long segments with large k)
+// the segment's W workgroups run cooperatively: all co-resident, they build one
+// whole-segment threshold from global histograms and a single candidate list.
 Plan make_plan(int seg_num, int64_t max_len, int k) {
   Plan plan{};
   plan.ok = false;
@@ -59,8 +62,14 @@ Plan make_plan(int seg_num, int64_t max_len, int k) {
   const int chunk = block * vpt * 8;
   const int64_t W = span <= chunk ? 1 : (span + chunk - 1) / chunk;
   const int kpad = next_pow2(k < 64 ? 64 : k);
-  const int cap_list = W > 1 ? next_pow2(2 * k > 128 ? 2 * k : 128) : 0;
-  if (W > 1 && W * static_cast<int64_t>(cap_list) > kCandArea) return plan;  // too long to merge
+  int cap_list = W > 1 ? next_pow2(2 * k > 128 ? 2 * k : 128) : 0;
+  bool cooperative = false;
+  if (W > 1 && W * static_cast<int64_t>(cap_list) > kCandArea) {
+    // Too many lists to merge in LDS: cooperative path, if the grid can be co-resident.
+    if (static_cast<int64_t>(seg_num) * W > kMaxCoopGroups) return plan;
+    cooperative = true;
+    cap_list = 0;
+  }
   if (static_cast<int64_t>(seg_num) * W > 0x7fffffff) return plan;
 
   plan.shape = KernelShape{block, vpt};
@@ -74,9 +83,12 @@ Plan make_plan(int seg_num, int64_t max_len, int k) {
   plan.lds_bytes = 256 * 4 + 256 * 4 + 32 * 4 + 16 * 4 + static_cast<size_t>(kCandArea) * 8 +
                    static_cast<size_t>(kpad) * 8 + static_cast<size_t>(rank_cap) * 4 +
                    static_cast<size_t>(block / 64) * kStageWords * 4;
+  plan.cooperative = cooperative;
   size_t ws = kAlign;                                        // alignment slack of the carve
   ws += align_up(static_cast<size_t>(seg_num) * 8, kAlign);  // arrival tickets
-  if (W > 1) {
+  if (cooperative) {
+    ws += static_cast<size_t>(seg_num) * kGroupBytes;        // per-segment group blocks
+  } else if (W > 1) {
     ws += align_up(static_cast<size_t>(seg_num) * W * 4, kAlign);               // list counts
     ws += static_cast<size_t>(seg_num) * W * static_cast<size_t>(cap_list) * 8;  // lists
   }
@@ -131,7 +143,10 @@ int run(const Plan& plan, const uint16_t* d_input, const int32_t* d_offsets, int
   size_t off = 0;
   p.tickets = reinterpret_cast<unsigned long long*>(ws + off);
   off += align_up(static_cast<size_t>(seg_num) * 8, kAlign);
-  if (plan.W > 1) {
+  p.cooperative = plan.cooperative ? 1 : 0;
+  if (plan.cooperative) {
+    p.groups = reinterpret_cast<unsigned char*>(ws + off);
+  } else if (plan.W > 1) {
     p.list_counts = reinterpret_cast<int32_t*>(ws + off);
     off += align_up(static_cast<size_t>(seg_num) * plan.W * 4, kAlign);
     p.lists = reinterpret_cast<unsigned long long*>(ws + off);

@@ -14,6 +14,20 @@ constexpr int kStageWords = 512;
 // Longest chunk one workgroup covers: 1024 threads x 16 vectors x 8 elements.
 constexpr int kMaxChunk = 1024 * 16 * 8;
 
+// Cooperative (whole-segment threshold) path: per-segment workspace block.
+//   bar   [kGroupWords]            epoch-tagged words (barriers, the zeroing flag)
+//   count [4]                      candidate list counters
+//   hist  [kGroupPasses][256]      per-pass global histograms (pass 0/1: threshold bytes,
+//                                  2..7: refinement digits)
+//   list  [kGroupCap]              the segment's candidate list (packed u64)
+constexpr int kGroupWords = 16;
+constexpr int kGroupPasses = 8;
+constexpr int kGroupCap = kCandArea;
+constexpr size_t kGroupBytes = kGroupWords * 8 + 16 + kGroupPasses * 256 * 4 + kGroupCap * 8;
+// Most co-resident workgroups the cooperative path asks for (one 1024-thread workgroup per CU
+// of an MI355X).
+constexpr int kMaxCoopGroups = 256;
+
 // Kernel parameter block of the fused segmented top-k kernel.  Every segment s covers the
 // element range [s0, s1) of `base` (a 16-byte aligned pointer); s0/s1 come from the int32
 // offsets when given, else from s * seg_len.  `elem0` is the element offset of the caller's
@@ -31,13 +45,14 @@ struct TopkParams {
   int32_t cap_list;             // workspace capacity of one chunk's published list
   int32_t cand_area;            // LDS entries of the candidate / merge area
   int32_t kpad;                 // LDS entries of the selection area (power of two >= k)
-  int32_t pad_;
+  int32_t cooperative;          // 1: whole-segment threshold across the segment's workgroups
   uint16_t* out_vals;           // [seg_num, k]
   int32_t* out_idx;             // [seg_num, k]
   unsigned long long* tickets;  // [seg_num] arrival words (epoch << 16 | count)
   int32_t* list_counts;         // [seg_num * W]
   unsigned long long* lists;    // [seg_num * W * cap_list] packed (key16 << 32 | index)
   unsigned long long epoch;     // 48-bit token unique to this call
+  unsigned char* groups;        // cooperative path: [seg_num] blocks of kGroupBytes
 };
 
 // One compiled instantiation of the fused kernel.
@@ -57,6 +72,7 @@ struct Plan {
   int kpad;
   size_t lds_bytes;
   size_t ws_bytes;  // workspace bytes (includes 256 bytes of alignment slack)
+  bool cooperative; // all W workgroups of a segment co-resident, one shared threshold
   bool ok;
 };
 

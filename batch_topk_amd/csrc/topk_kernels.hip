@@ -393,6 +393,82 @@ __device__ __forceinline__ bool arrive_last(u64* ticket, u64 epoch, int arrivals
 
 __device__ __forceinline__ void wait_vector_memory() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// ------------------------------------------------------------------------------ cooperative
+
+// Per-segment block of the cooperative path (layout in topk_common.hpp).
+struct GroupWs {
+  u64* word;   // [kGroupWords] epoch-tagged words: 0 zeroing done, 1.. barriers
+  u32* count;  // [4] candidate list counters
+  u32* hist;   // [kGroupPasses][256]
+  u64* list;   // [kGroupCap]
+};
+
+__device__ __forceinline__ GroupWs group_ws(const TopkParams& p, int seg) {
+  unsigned char* b = p.groups + static_cast<size_t>(seg) * kGroupBytes;
+  GroupWs g;
+  g.word = reinterpret_cast<u64*>(b);
+  g.count = reinterpret_cast<u32*>(b + kGroupWords * 8);
+  g.hist = reinterpret_cast<u32*>(b + kGroupWords * 8 + 16);
+  g.list = reinterpret_cast<u64*>(b + kGroupWords * 8 + 16 + kGroupPasses * 256 * 4);
+  return g;
+}
+
+// Tagged counter words: tag44 << 20 | count20, where tag is the call's epoch.  A word with
+// another tag is stale (earlier call, or uninitialised workspace) and reads as zero, so the
+// words need no clearing.
+constexpr u64 kTagMask = (1ull << 44) - 1;
+__device__ __forceinline__ u32 tagged_value(u64 word, u64 tag) {
+  return (word >> 20) == tag ? static_cast<u32>(word & 0xfffffu) : 0u;
+}
+__device__ __forceinline__ void tagged_add(u64* word, u64 tag, u32 add) {
+  u64 old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    const u64 next = (tag << 20) | (tagged_value(old, tag) + add);
+    if (__hip_atomic_compare_exchange_strong(word, &old, next, __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+      return;
+    }
+  }
+}
+// Thread 0 polls until the word reaches `target` (bounded: a launch that is not co-resident
+// cannot happen under a cooperative launch, but no wave may spin forever).
+constexpr u32 kGroupSpinLimit = 1u << 22;
+__device__ __forceinline__ void tagged_wait(u64* word, u64 tag, u32 target) {
+  for (u32 spin = 0; spin < kGroupSpinLimit; ++spin) {
+    if (tagged_value(__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), tag) >= target) {
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// All `arrivals` workgroups of a segment meet here.  Every thread first waits for its own
+// cross-workgroup writes (agent-scope atomics, device-coherent) to complete; after the
+// barrier the workgroup's agent-scope loads see every other workgroup's writes.
+__device__ __forceinline__ void group_barrier(u64* word, u64 tag, int arrivals) {
+  wait_vector_memory();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    tagged_add(word, tag, 1u);
+    tagged_wait(word, tag, static_cast<u32>(arrivals));
+  }
+  __syncthreads();
+}
+
+// Adds this workgroup's LDS histogram to the segment's global one (nonzero bins only), meets
+// the other workgroups, and loads the summed histogram back into LDS.
+template <int BLOCK>
+__device__ void group_histogram(u32* lds_hist, u32* global_hist, u64* word, u64 tag, int arrivals) {
+  const int tid = threadIdx.x;
+  if (tid < 256) {
+    const u32 c = lds_hist[tid];
+    if (c) __hip_atomic_fetch_add(global_hist + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  group_barrier(word, tag, arrivals);
+  if (tid < 256) lds_hist[tid] = __hip_atomic_load(global_hist + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+}
+
 // Nontemporal 16-byte load at a 32-bit byte offset from a wave-uniform base (so the
 // address stays in the scalar base + 32-bit vector offset form).
 __device__ __forceinline__ uint4 load_nt(const unsigned char* base, u32 byte_off) {
@@ -415,7 +491,7 @@ __device__ __forceinline__ u32 vec_min2(const uint4& x) {
 
 // ------------------------------------------------------------------------------ the kernel
 
-template <int BLOCK, int VPT>
+template <int BLOCK, int VPT, bool COOP>
 __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   constexpr int NW = BLOCK / 64;
   constexpr int CH = BLOCK * VPT * 8;
@@ -474,6 +550,24 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   const int lo = static_cast<int>(c0 - cb);  // valid chunk positions are [lo, hi)
   const int hi = static_cast<int>(c1 - cb);
   const u32 idx_base = static_cast<u32>(cb - s0);  // segment index = idx_base + position
+  const int need = COOP ? kk : kc;  // rank the threshold must cover (segment or chunk)
+
+  // Cooperative path: workgroup 0 clears the segment's global histograms and counters of this
+  // call before loading its chunk, then raises the zeroing flag.
+  const u64 tag = p.epoch & kTagMask;
+  GroupWs g{};
+  if constexpr (COOP) {
+    g = group_ws(p, seg);
+    if (w == 0) {
+      for (int i = tid; i < kGroupPasses * 256; i += BLOCK) {
+        __hip_atomic_store(g.hist + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (tid < 4) __hip_atomic_store(g.count + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wait_vector_memory();
+      __syncthreads();
+      if (tid == 0) __hip_atomic_store(g.word, (tag << 20) | 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 
   // ---- 1. load the chunk: all nontemporal 16-byte loads issued before any is consumed; a
   // block with no element of the chunk re-reads the chunk's first block (always in bounds).
@@ -523,13 +617,19 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   if (tid < 256) sm.hist2[tid] = 0;
   if (tid == 0) sm.scal[4] = 0;  // candidate list counter
   __syncthreads();
-  if (wid == 0) wave_find_bucket(sm.hist, kc, sm.scal + 8, lane);
+  if constexpr (COOP) {
+    if (tid == 0) tagged_wait(g.word, tag, 1u);  // the global histograms are cleared
+    __syncthreads();
+    group_histogram<BLOCK>(sm.hist, g.hist, g.word + 1, tag, Ws);
+  }
+  if (wid == 0) wave_find_bucket(sm.hist, need, sm.scal + 8, lane);
   __syncthreads();
   TOPK_TRACE(2);
   const u32 b1 = static_cast<u32>(sm.scal[8]);
   if ((best_key >> 8) == b1) atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
   __syncthreads();
-  if (wid == 0) wave_find_bucket(sm.hist2, kc - sm.scal[9], sm.scal + 12, lane);
+  if constexpr (COOP) group_histogram<BLOCK>(sm.hist2, g.hist + 256, g.word + 2, tag, Ws);
+  if (wid == 0) wave_find_bucket(sm.hist2, need - sm.scal[9], sm.scal + 12, lane);
   __syncthreads();
   const u32 T = (b1 << 8) | static_cast<u32>(sm.scal[12]);
   TOPK_TRACE(4);
@@ -684,6 +784,107 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
 
   int C = all_mode ? 0 : sm.scal[4];
   const bool overflow = C > kArea;
+  // Re-reads the chunk from memory and calls fn(raw bits, chunk position) for every element
+  // in [lo, hi): the refinement passes do not keep the fast path's registers live.
+  auto for_each_element = [&](auto&& fn) {
+#pragma unroll 1
+    for (int j = 0; j < VPT; ++j) {
+      const int pos0 = (j * BLOCK + tid) * 8;
+      if (pos0 < hi && pos0 + 8 > lo) {
+        const uint4 x = *reinterpret_cast<const uint4*>(cptr + static_cast<u32>(pos0) * 2u);
+        const u32 w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int pos = pos0 + e;
+          if (pos >= lo && pos < hi) fn((w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu, pos);
+        }
+      }
+    }
+  };
+
+  if constexpr (COOP) {
+    // ---- 4c. cooperative segment: one candidate list for the whole segment.  Every
+    // workgroup appends its list (an overflowing or threshold-less chunk pushes the count past
+    // the capacity instead), the workgroups meet, and workgroup 0 selects from the list.
+    const u32 contrib = (all_mode || overflow) ? static_cast<u32>(kGroupCap) + 1u : static_cast<u32>(C);
+    if (tid == 0) {
+      sm.scal[6] = static_cast<int>(
+          __hip_atomic_fetch_add(g.count, contrib, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    __syncthreads();
+    u32 base = static_cast<u32>(sm.scal[6]);
+    if (contrib <= static_cast<u32>(kGroupCap) && base + contrib <= static_cast<u32>(kGroupCap)) {
+      for (u32 i = tid; i < contrib; i += BLOCK) {
+        __hip_atomic_store(g.list + base + i, sm.area[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    group_barrier(g.word + 3, tag, Ws);
+    u32 total = __hip_atomic_load(g.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (total > static_cast<u32>(kGroupCap)) {
+      // ---- 4d. the list would not fit: exact radix refinement over the whole segment of
+      // Q = key16 << 32 | index32 among the elements with key <= T, one global histogram per
+      // 8-bit digit, until at most kGroupCap elements are <= the bound.
+      u64 prefix = 0, pmask = 0;
+      int rneed = kk;
+      int pass = 0;
+      for (int shift = 40; shift >= 0; shift -= 8, ++pass) {
+        for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
+        __syncthreads();
+        for_each_element([&](u32 b, int pos) {
+          const u32 key = desc_key(b);
+          const u64 Q = (static_cast<u64>(key) << 32) | (idx_base + static_cast<u32>(pos));
+          if (key <= T && (Q & pmask) == prefix) atomicAdd(&sm.hist[(Q >> shift) & 255u], 1u);
+        });
+        __syncthreads();
+        group_histogram<BLOCK>(sm.hist, g.hist + (2 + pass) * 256, g.word + 4 + pass, tag, Ws);
+        if (wid == 0) wave_find_bucket(sm.hist, rneed, sm.scal, lane);
+        __syncthreads();
+        const int b = sm.scal[0];
+        const int before = sm.scal[1];
+        const int cnt = sm.scal[2];
+        __syncthreads();
+        rneed -= before;
+        prefix |= static_cast<u64>(b) << shift;
+        pmask |= 0xffull << shift;
+        if ((kk - rneed) + cnt <= kGroupCap) break;
+      }
+      const u64 bound = prefix | (~pmask & 0xFFFFFFFFFFFFull);
+      if (tid == 0) sm.scal[4] = 0;
+      __syncthreads();
+      for_each_element([&](u32 b, int pos) {
+        const u32 key = desc_key(b);
+        const u32 idx = idx_base + static_cast<u32>(pos);
+        const u64 Q = (static_cast<u64>(key) << 32) | idx;
+        if (key <= T && Q <= bound) {
+          const int slot = atomicAdd(&sm.scal[4], 1);
+          if (slot < kArea) sm.area[slot] = pack_candidate(b, idx);
+        }
+      });
+      __syncthreads();
+      const u32 c2 = static_cast<u32>(sm.scal[4] < kArea ? sm.scal[4] : kArea);
+      if (tid == 0) {
+        sm.scal[6] = static_cast<int>(
+            __hip_atomic_fetch_add(g.count + 1, c2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      }
+      __syncthreads();
+      base = static_cast<u32>(sm.scal[6]);
+      for (u32 i = tid; i < c2; i += BLOCK) {
+        if (base + i < static_cast<u32>(kGroupCap)) {
+          __hip_atomic_store(g.list + base + i, sm.area[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      group_barrier(g.word + 10, tag, Ws);
+      total = __hip_atomic_load(g.count + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      total = total < static_cast<u32>(kGroupCap) ? total : static_cast<u32>(kGroupCap);
+    }
+    if (w != 0) return;
+    for (u32 i = tid; i < total; i += BLOCK) {
+      sm.area[i] = __hip_atomic_load(g.list + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    finalize_segment<BLOCK>(p, sm, static_cast<int>(total), kk, n, seg);
+    return;
+  }
   if (all_mode && nc <= kArea) {
     // Every in-range element, at its position: no counting needed.
 #pragma unroll
@@ -703,21 +904,6 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
     // Radix select over P = key16 << 17 | position17 among in-range elements with key <= T,
     // until at most kArea values are <= the bound.  The chunk is re-read from memory for each
     // pass, so the registers of the fast path are not kept live for it.
-    auto for_each_element = [&](auto&& fn) {
-#pragma unroll 1
-      for (int j = 0; j < VPT; ++j) {
-        const int pos0 = (j * BLOCK + tid) * 8;
-        if (pos0 < hi && pos0 + 8 > lo) {
-          const uint4 x = *reinterpret_cast<const uint4*>(cptr + static_cast<u32>(pos0) * 2u);
-          const u32 w4[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int pos = pos0 + e;
-            if (pos >= lo && pos < hi) fn((w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu, pos);
-          }
-        }
-      }
-    };
     u64 prefix = 0, pmask = 0;
     int need = kc;
     for (int shift = 32; shift >= 0; shift -= 8) {
@@ -819,8 +1005,20 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
 template <int BLOCK, int VPT>
 int launch_shape(const Plan& plan, const TopkParams& params, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(params.seg_num) * plan.W));
-  hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT>), grid, dim3(BLOCK),
+  hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT, false>), grid, dim3(BLOCK),
                      static_cast<unsigned>(plan.lds_bytes), stream, params);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Cooperative launch: the runtime refuses (hipErrorCooperativeLaunchTooLarge) a grid that
+// cannot be co-resident, so the workgroups' barriers always complete.
+int launch_cooperative(const Plan& plan, TopkParams params, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(params.seg_num) * plan.W));
+  void* args[] = {&params};
+  const hipError_t e = hipLaunchCooperativeKernel(
+      reinterpret_cast<const void*>(&segmented_topk_kernel<1024, 16, true>), grid, dim3(1024), args,
+      static_cast<unsigned>(plan.lds_bytes), stream);
+  if (e != hipSuccess) return static_cast<int>(e);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -830,6 +1028,10 @@ int launch_segmented_topk(const Plan& plan, const TopkParams& params, void* stre
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int b = plan.shape.block;
   const int vpt = plan.shape.vpt;
+  if (plan.cooperative) {
+    if (b != 1024 || vpt != 16) return static_cast<int>(hipErrorInvalidValue);
+    return launch_cooperative(plan, params, s);
+  }
   if (b == 256 && vpt == 2) return launch_shape<256, 2>(plan, params, s);
   if (b == 256 && vpt == 4) return launch_shape<256, 4>(plan, params, s);
   if (b == 256 && vpt == 8) return launch_shape<256, 8>(plan, params, s);

@@ -197,3 +197,52 @@ def test_varlen_segment_longer_than_declared_max_is_padded():
     exp = O.batch_topk_half(bits, 10, offsets=offsets.astype(np.int64))
     assert np.array_equal(idx[0], exp[1][0]) and np.array_equal(idx[2], exp[1][2])
     assert np.all(idx[1] == -1) and np.all(vals[1] == 0xFFFF)
+
+
+# ------------------------------------------------------------------ cooperative path
+# Segments longer than one workgroup's chunk with k too large for the LDS merge of per-chunk
+# lists: every workgroup of the segment shares one threshold from global histograms.
+
+def _coop_rows(name, n):
+    rng = np.random.default_rng(len(name) * 7 + n % 97)
+    if name == "normal":
+        return rng.standard_normal((1, n)).astype(np.float16).view(np.uint16)
+    if name == "all_equal":
+        return np.full((1, n), 0x3C00, dtype=np.uint16)
+    if name == "all_nan":
+        return np.tile(np.array([0x7E00, 0xFE00, 0x7C01, 0xFFFF], dtype=np.uint16), (1, n // 4))
+    if name == "sorted_ascending":
+        return np.sort(rng.standard_normal((1, n)).astype(np.float16), axis=1).view(np.uint16)
+    if name == "sorted_descending":
+        return np.sort(rng.standard_normal((1, n)).astype(np.float16), axis=1)[:, ::-1].copy().view(np.uint16)
+    if name == "few_distinct":
+        return (rng.integers(-4, 5, size=(1, n)) * 0.25).astype(np.float16).view(np.uint16)
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name", ["normal", "all_equal", "all_nan", "sorted_ascending",
+                                  "sorted_descending", "few_distinct"])
+def test_cooperative_single_segment(name):
+    bits = _coop_rows(name, 1_000_000)
+    for k in (300, 1024):
+        vals, idx = check_fixed(bits, k, f"cooperative {name}")
+        assert_properties(bits, vals, idx, k, [bits.shape[1]])
+
+
+def test_cooperative_several_segments():
+    rng = np.random.default_rng(31)
+    bits = rng.standard_normal((3, 300_001)).astype(np.float16).view(np.uint16)
+    bits[1, 1000:200000] = 0x4400  # a long run of equal large values in one segment
+    check_fixed(bits, 512, "cooperative 3 segments", elem_offset=3)
+
+
+def test_cooperative_variable_segments():
+    rng = np.random.default_rng(37)
+    lengths = np.array([400_000, 5, 0, 300_000, 150_000, 131_072, 131_073], dtype=np.int64)
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    bits = rng.standard_normal(int(offsets[-1])).astype(np.float16).view(np.uint16)
+    bits[offsets[3]:offsets[3] + 50_000] = 0x3C00
+    announce("cooperative variable-length segments k=300")
+    got = run_segmented(bits, offsets, 300, 400_000, poison=0x5A)
+    exp = O.batch_topk_half(bits, 300, offsets=offsets.astype(np.int64), threads=THREADS)
+    assert_same(got, exp, "cooperative varlen")
