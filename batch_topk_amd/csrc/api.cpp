@@ -87,7 +87,7 @@ Plan make_plan(int seg_num, int64_t max_len, int k) {
   size_t ws = kAlign;                                        // alignment slack of the carve
   ws += align_up(static_cast<size_t>(seg_num) * 8, kAlign);  // arrival tickets
   if (cooperative) {
-    ws += static_cast<size_t>(seg_num) * kGroupBytes;        // per-segment group blocks
+    ws += static_cast<size_t>(seg_num) * group_layout(static_cast<int>(W)).bytes;  // group blocks
   } else if (W > 1) {
     ws += align_up(static_cast<size_t>(seg_num) * W * 4, kAlign);               // list counts
     ws += static_cast<size_t>(seg_num) * W * static_cast<size_t>(cap_list) * 8;  // lists

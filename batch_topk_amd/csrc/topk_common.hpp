@@ -14,16 +14,42 @@ constexpr int kStageWords = 512;
 // Longest chunk one workgroup covers: 1024 threads x 16 vectors x 8 elements.
 constexpr int kMaxChunk = 1024 * 16 * 8;
 
-// Cooperative (whole-segment threshold) path: per-segment workspace block.
-//   bar   [kGroupWords]            epoch-tagged words (barriers, the zeroing flag)
-//   count [4]                      candidate list counters
-//   hist  [kGroupPasses][256]      per-pass global histograms (pass 0/1: threshold bytes,
-//                                  2..7: refinement digits)
-//   list  [kGroupCap]              the segment's candidate list (packed u64)
-constexpr int kGroupWords = 16;
-constexpr int kGroupPasses = 8;
-constexpr int kGroupCap = kCandArea;
-constexpr size_t kGroupBytes = kGroupWords * 8 + 16 + kGroupPasses * 256 * 4 + kGroupCap * 8;
+// Cooperative (whole-segment threshold) path: per-segment workspace block of a segment split
+// over W workgroups.  Nothing in it needs clearing before a call except the histograms, which
+// workgroup 0 clears at the start of the call:
+//   flag    u64                       epoch-tagged "histograms cleared" word
+//   arrive  u64 [kGroupBarriers][W]   per-barrier arrival slots (a slot holding this call's
+//                                     epoch has arrived)
+//   counts  u64 [2][W]                epoch-tagged list lengths (tag44 << 20 | length)
+//   hist    u32 [2][kGroupCopies][256] threshold histograms, each spread over kGroupCopies
+//                                     copies so that few workgroups add to one address
+//   rhist   u32 [6][256]              refinement digit histograms
+//   lists   u64 [W][kCandArea]        every workgroup's candidate list
+constexpr int kGroupBarriers = 10;
+constexpr int kGroupCopies = 16;
+constexpr int kGroupCap = kCandArea;  // longest whole-segment list the final ranking takes
+struct GroupLayout {
+  size_t flag, arrive, counts, hist, rhist, lists, bytes;
+};
+constexpr size_t group_align(size_t x) { return (x + 127) / 128 * 128; }
+constexpr GroupLayout group_layout(int W) {
+  GroupLayout L{};
+  size_t off = 0;
+  L.flag = off;
+  off += 128;
+  L.arrive = off;
+  off += group_align(static_cast<size_t>(kGroupBarriers) * W * 8);
+  L.counts = off;
+  off += group_align(static_cast<size_t>(2) * W * 8);
+  L.hist = off;
+  off += static_cast<size_t>(2) * kGroupCopies * 256 * 4;
+  L.rhist = off;
+  off += static_cast<size_t>(6) * 256 * 4;
+  L.lists = off;
+  off += static_cast<size_t>(W) * kCandArea * 8;
+  L.bytes = off;
+  return L;
+}
 // Most co-resident workgroups the cooperative path asks for (one 1024-thread workgroup per CU
 // of an MI355X).
 constexpr int kMaxCoopGroups = 256;
@@ -52,7 +78,7 @@ struct TopkParams {
   int32_t* list_counts;         // [seg_num * W]
   unsigned long long* lists;    // [seg_num * W * cap_list] packed (key16 << 32 | index)
   unsigned long long epoch;     // 48-bit token unique to this call
-  unsigned char* groups;        // cooperative path: [seg_num] blocks of kGroupBytes
+  unsigned char* groups;        // cooperative path: [seg_num] blocks of group_layout(W).bytes
 };
 
 // One compiled instantiation of the fused kernel.

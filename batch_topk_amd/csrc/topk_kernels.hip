@@ -5,8 +5,8 @@
 // nontemporal 16-byte loads that are all issued up front, into registers.  Everything after
 // the load runs on registers and LDS, overlapped with the loads still in flight:
 //
-//   1. thread best     over the first half of the vectors: packed int16 max/min trees over the
-//                      raw fp16 bits (v_pk_max_i16 / v_pk_min_i16).  The int16 max is the best
+//   1. thread best     packed int16 max/min trees over the raw fp16 bits of all the thread's
+//                      vectors (v_pk_max_i16 / v_pk_min_i16).  The int16 max is the best
 //                      non-negative-sign element, the int16 min the best negative-sign one;
 //                      whichever applies is a real element of the thread (or, for a NaN, a
 //                      worse one), which is all the threshold needs.
@@ -14,23 +14,28 @@
 //                      exactly with two LDS histogram passes (high byte, then low byte inside
 //                      the boundary bucket) and DPP prefix scans.  At least kc real elements
 //                      have key <= T, so every element of the chunk's top kc does.
-//   3. filter          only a lane whose best key is <= T can hold a candidate.  Each wave
-//                      copies those lanes' words into its LDS staging area and tests them one
-//                      word per lane, so the work follows the candidate lanes (a few per wave
-//                      on logits), not the chunk.  Hits reserve their LDS slots with one atomic
-//                      per wave and step and are written at ballot/mbcnt offsets, packed as
+//   3. filter          only a vector whose int16 max reaches T can hold a candidate.  A wave
+//                      copies its lanes' passing vectors into an LDS staging list and tests
+//                      them one vector per lane; a wave prefix sum places the hits, which one
+//                      LDS atomic per wave reserves in the list, packed as
 //                      (key16 << 48 | index32 << 16 | raw16): one u64 compare orders
 //                      (key, index), and the raw bits ride along to the output.
 //                      If the list overflows (ties, all-equal rows), an exact radix refinement
 //                      over (key16, position17), re-reading the chunk, rebuilds it.
-//   4. selection       small sets: every wave holds the whole list in registers and ranks its
-//                      share by ballot counts; larger sets: LDS radix select over the packed
-//                      values down to exactly k, then rank counting.
+//   4. selection       small sets: every wave holds the whole list in registers, ranks its
+//                      share by ballot counts and writes it; larger sets: LDS radix select over
+//                      the packed values down to exactly k, then rank counting.
 //   5. output          index and raw value bits of each selected candidate.
 //
-// Segments longer than one chunk are split over W workgroups; each publishes its list to the
-// workspace and the last to arrive (an epoch-tagged arrival counter, so the workspace needs no
-// initialisation) merges the lists with step 4.
+// Segments longer than one chunk are split over W workgroups.  While the W lists fit one LDS
+// merge, each workgroup publishes its list to the workspace and the last to arrive (an
+// epoch-tagged arrival counter, so the workspace needs no initialisation) merges them with
+// step 4.  Beyond that (long segments with large k) the W workgroups run cooperatively, all
+// co-resident: the threshold histograms of step 2 are summed over the whole segment in global
+// memory, each workgroup filters its chunk against the one segment threshold, and every
+// workgroup gathers the segment's candidate list and ranks a share of it.  Workgroups meet at
+// barriers made of per-workgroup arrival slots holding the call's epoch; an exact global
+// radix refinement over (key16, index32) takes over when the list would not fit.
 //
 // Ordering contract (reference include/batch_topk_types.cuh:70-82,100-113 and
 // include/type_codec.cuh:9-38): ascending (desc_key, index), where desc_key maps every NaN
@@ -38,7 +43,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
+#include <cstdlib>
 
 #include "topk_common.hpp"
 
@@ -397,76 +404,172 @@ __device__ __forceinline__ void wait_vector_memory() { asm volatile("s_waitcnt v
 
 // Per-segment block of the cooperative path (layout in topk_common.hpp).
 struct GroupWs {
-  u64* word;   // [kGroupWords] epoch-tagged words: 0 zeroing done, 1.. barriers
-  u32* count;  // [4] candidate list counters
-  u32* hist;   // [kGroupPasses][256]
-  u64* list;   // [kGroupCap]
+  u64* flag;    // epoch-tagged "histograms cleared"
+  u64* arrive;  // [kGroupBarriers][W] arrival slots
+  u64* counts;  // [2][W] epoch-tagged list lengths
+  u32* hist;    // [2][kGroupCopies][256]
+  u32* rhist;   // [6][256]
+  u64* lists;   // [W][kCandArea]
 };
 
 __device__ __forceinline__ GroupWs group_ws(const TopkParams& p, int seg) {
-  unsigned char* b = p.groups + static_cast<size_t>(seg) * kGroupBytes;
+  const GroupLayout L = group_layout(p.chunks_per_seg);
+  unsigned char* b = p.groups + static_cast<size_t>(seg) * L.bytes;
   GroupWs g;
-  g.word = reinterpret_cast<u64*>(b);
-  g.count = reinterpret_cast<u32*>(b + kGroupWords * 8);
-  g.hist = reinterpret_cast<u32*>(b + kGroupWords * 8 + 16);
-  g.list = reinterpret_cast<u64*>(b + kGroupWords * 8 + 16 + kGroupPasses * 256 * 4);
+  g.flag = reinterpret_cast<u64*>(b + L.flag);
+  g.arrive = reinterpret_cast<u64*>(b + L.arrive);
+  g.counts = reinterpret_cast<u64*>(b + L.counts);
+  g.hist = reinterpret_cast<u32*>(b + L.hist);
+  g.rhist = reinterpret_cast<u32*>(b + L.rhist);
+  g.lists = reinterpret_cast<u64*>(b + L.lists);
   return g;
 }
 
-// Tagged counter words: tag44 << 20 | count20, where tag is the call's epoch.  A word with
-// another tag is stale (earlier call, or uninitialised workspace) and reads as zero, so the
-// words need no clearing.
-constexpr u64 kTagMask = (1ull << 44) - 1;
-__device__ __forceinline__ u32 tagged_value(u64 word, u64 tag) {
-  return (word >> 20) == tag ? static_cast<u32>(word & 0xfffffu) : 0u;
+__device__ __forceinline__ u64 load_agent(const u64* a) {
+  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void tagged_add(u64* word, u64 tag, u32 add) {
-  u64 old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (;;) {
-    const u64 next = (tag << 20) | (tagged_value(old, tag) + add);
-    if (__hip_atomic_compare_exchange_strong(word, &old, next, __ATOMIC_RELAXED,
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-      return;
-    }
-  }
+__device__ __forceinline__ u32 load_agent(const u32* a) {
+  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Thread 0 polls until the word reaches `target` (bounded: a launch that is not co-resident
-// cannot happen under a cooperative launch, but no wave may spin forever).
-constexpr u32 kGroupSpinLimit = 1u << 22;
-__device__ __forceinline__ void tagged_wait(u64* word, u64 tag, u32 target) {
-  for (u32 spin = 0; spin < kGroupSpinLimit; ++spin) {
-    if (tagged_value(__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), tag) >= target) {
-      return;
-    }
-    __builtin_amdgcn_s_sleep(2);
-  }
+__device__ __forceinline__ void store_agent(u64* a, u64 v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(u32* a, u32 v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// All `arrivals` workgroups of a segment meet here.  Every thread first waits for its own
-// cross-workgroup writes (agent-scope atomics, device-coherent) to complete; after the
-// barrier the workgroup's agent-scope loads see every other workgroup's writes.
-__device__ __forceinline__ void group_barrier(u64* word, u64 tag, int arrivals) {
+// Epoch-tagged words (tag44 << 20 | value20): a word carrying another tag is stale (an
+// earlier call, or uninitialised workspace) and reads as "absent".
+constexpr u64 kTagMask = (1ull << 44) - 1;
+constexpr u32 kAbsent = 0xffffffffu;
+__device__ __forceinline__ u32 tagged_value(u64 word, u64 tag) {
+  return (word >> 20) == tag ? static_cast<u32>(word & 0xfffffu) : kAbsent;
+}
+
+// Every bounded wait of the cooperative path: no wave may spin forever, even if the grid were
+// not co-resident (the launcher checks that it is).
+constexpr u32 kGroupSpinLimit = 1u << 22;
+
+// All `arrivals` workgroups of a segment meet here.  Each writes this call's epoch into its
+// own arrival slot (no two workgroups touch one address), and threads 0..arrivals-1 each wait
+// for one slot.  Every thread first waits for its own cross-workgroup writes (agent-scope
+// atomics, device-coherent) to complete; after the barrier the workgroup's agent-scope loads
+// see every other workgroup's writes.
+__device__ __forceinline__ void group_barrier(u64* slots, u64 epoch, int w, int arrivals) {
   wait_vector_memory();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    tagged_add(word, tag, 1u);
-    tagged_wait(word, tag, static_cast<u32>(arrivals));
+  const int tid = threadIdx.x;
+  if (tid == 0) store_agent(slots + w, epoch);
+  if (tid < arrivals) {
+    for (u32 spin = 0; spin < kGroupSpinLimit; ++spin) {
+      if (load_agent(slots + tid) == epoch) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
   }
   __syncthreads();
 }
 
-// Adds this workgroup's LDS histogram to the segment's global one (nonzero bins only), meets
-// the other workgroups, and loads the summed histogram back into LDS.
+// Threshold histogram of the whole segment: every workgroup adds its LDS histogram to copy
+// (w mod kGroupCopies) of the global one (nonzero bins only), the workgroups meet, and each
+// loads the sum of the copies back into LDS (four copies per thread, partial sums staged in
+// `scratch`, 1024 words of LDS).
 template <int BLOCK>
-__device__ void group_histogram(u32* lds_hist, u32* global_hist, u64* word, u64 tag, int arrivals) {
+__device__ void group_histogram(u32* lds_hist, u32* ghist, u32* scratch, u64* slots, u64 epoch, int w,
+                                int arrivals) {
+  static_assert(BLOCK == 1024, "the copy sum assumes 4 threads per bin");
   const int tid = threadIdx.x;
   if (tid < 256) {
     const u32 c = lds_hist[tid];
-    if (c) __hip_atomic_fetch_add(global_hist + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (c) {
+      __hip_atomic_fetch_add(ghist + (w % kGroupCopies) * 256 + tid, c, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
-  group_barrier(word, tag, arrivals);
-  if (tid < 256) lds_hist[tid] = __hip_atomic_load(global_hist + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  group_barrier(slots, epoch, w, arrivals);
+  const int bin = tid & 255;
+  const int q = tid >> 8;
+  u32 part = 0;
+#pragma unroll
+  for (int c = 0; c < kGroupCopies / 4; ++c) part += load_agent(ghist + (q + 4 * c) * 256 + bin);
+  scratch[q * 256 + bin] = part;
   __syncthreads();
+  if (tid < 256) lds_hist[tid] = scratch[tid] + scratch[256 + tid] + scratch[512 + tid] + scratch[768 + tid];
+  __syncthreads();
+}
+
+// Single-copy variant for the (rare) refinement digits.
+template <int BLOCK>
+__device__ void group_histogram_single(u32* lds_hist, u32* ghist, u64* slots, u64 epoch, int w,
+                                       int arrivals) {
+  const int tid = threadIdx.x;
+  if (tid < 256) {
+    const u32 c = lds_hist[tid];
+    if (c) __hip_atomic_fetch_add(ghist + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  group_barrier(slots, epoch, w, arrivals);
+  if (tid < 256) lds_hist[tid] = load_agent(ghist + tid);
+  __syncthreads();
+}
+
+// Whole-segment candidate list from the workgroups' lists: reads the W tagged lengths,
+// prefix-sums them (wave 0), and, if no list overflowed and the total fits kGroupCap, gathers
+// every entry into `area`.  Returns the total, or kAbsent when the list cannot be formed.
+template <int BLOCK>
+__device__ u32 group_gather(const u64* counts, const u64* lists, u64 tag, int arrivals, u64* area,
+                            int* cnt, int* pre, int* scal) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  if (tid < 256) {
+    u32 c = 0;
+    if (tid < arrivals) {
+      c = tagged_value(load_agent(counts + tid), tag);
+      if (c > static_cast<u32>(kCandArea)) c = static_cast<u32>(kGroupCap) + 1u;  // overflow or absent
+    }
+    cnt[tid] = static_cast<int>(c);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int c0 = cnt[4 * lane], c1 = cnt[4 * lane + 1], c2 = cnt[4 * lane + 2], c3 = cnt[4 * lane + 3];
+    const u32 sum = static_cast<u32>(c0 + c1 + c2 + c3);
+    const u32 incl = wave_inclusive_scan(sum);
+    const u32 excl = incl - sum;
+    pre[4 * lane] = static_cast<int>(excl);
+    pre[4 * lane + 1] = static_cast<int>(excl + c0);
+    pre[4 * lane + 2] = static_cast<int>(excl + c0 + c1);
+    pre[4 * lane + 3] = static_cast<int>(excl + c0 + c1 + c2);
+    if (lane == 63) scal[0] = static_cast<int>(incl);
+  }
+  __syncthreads();
+  const u32 total = static_cast<u32>(scal[0]);
+  if (total > static_cast<u32>(kGroupCap)) return kAbsent;
+  for (u32 i = tid; i < total; i += BLOCK) {
+    int lo_t = 0, hi_t = arrivals;  // last t with pre[t] <= i
+    while (hi_t - lo_t > 1) {
+      const int mid = (lo_t + hi_t) >> 1;
+      if (static_cast<u32>(pre[mid]) <= i) lo_t = mid; else hi_t = mid;
+    }
+    area[i] = load_agent(lists + static_cast<size_t>(lo_t) * kCandArea + (i - static_cast<u32>(pre[lo_t])));
+  }
+  __syncthreads();
+  return total;
+}
+
+// Ranks the candidates list[c0, c1) against all M unique entries of `list` (LDS) and writes
+// those of rank < kk to the output row: one wave per candidate, each lane comparing every
+// 64th entry, the counts summed across the wave.
+template <int BLOCK>
+__device__ void rank_range_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
+                                 int kk, int c0, int c1) {
+  constexpr int NW = BLOCK / 64;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  for (int i = c0 + wid; i < c1; i += NW) {
+    const u64 P = list[i];
+    u32 c = 0;
+    for (int j = lane; j < M; j += 64) c += list[j] < P ? 1u : 0u;
+    const u32 r = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_scan(c)), 63));
+    if (lane == 0 && r < static_cast<u32>(kk)) write_rank(p, n, seg, static_cast<int>(r), P);
+  }
 }
 
 // Nontemporal 16-byte load at a 32-bit byte offset from a wave-uniform base (so the
@@ -552,20 +655,19 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   const u32 idx_base = static_cast<u32>(cb - s0);  // segment index = idx_base + position
   const int need = COOP ? kk : kc;  // rank the threshold must cover (segment or chunk)
 
-  // Cooperative path: workgroup 0 clears the segment's global histograms and counters of this
-  // call before loading its chunk, then raises the zeroing flag.
-  const u64 tag = p.epoch & kTagMask;
+  // Cooperative path: workgroup 0 clears the segment's global histograms of this call before
+  // loading its chunk, then raises the epoch-tagged "cleared" flag.
+  const u64 epoch = p.epoch;
+  const u64 tag = epoch & kTagMask;
   GroupWs g{};
   if constexpr (COOP) {
     g = group_ws(p, seg);
     if (w == 0) {
-      for (int i = tid; i < kGroupPasses * 256; i += BLOCK) {
-        __hip_atomic_store(g.hist + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (tid < 4) __hip_atomic_store(g.count + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = tid; i < 2 * kGroupCopies * 256; i += BLOCK) store_agent(g.hist + i, 0u);
+      for (int i = tid; i < 6 * 256; i += BLOCK) store_agent(g.rhist + i, 0u);
       wait_vector_memory();
       __syncthreads();
-      if (tid == 0) __hip_atomic_store(g.word, (tag << 20) | 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0) store_agent(g.flag, (tag << 20) | 1u);
     }
   }
 
@@ -618,9 +720,15 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   if (tid == 0) sm.scal[4] = 0;  // candidate list counter
   __syncthreads();
   if constexpr (COOP) {
-    if (tid == 0) tagged_wait(g.word, tag, 1u);  // the global histograms are cleared
+    if (tid == 0) {  // the global histograms are cleared
+      for (u32 spin = 0; spin < kGroupSpinLimit; ++spin) {
+        if (tagged_value(load_agent(g.flag), tag) == 1u) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
     __syncthreads();
-    group_histogram<BLOCK>(sm.hist, g.hist, g.word + 1, tag, Ws);
+    group_histogram<BLOCK>(sm.hist, g.hist, sm.stage, g.arrive, epoch, w, Ws);
+    TOPK_TRACE(8);
   }
   if (wid == 0) wave_find_bucket(sm.hist, need, sm.scal + 8, lane);
   __syncthreads();
@@ -628,7 +736,10 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   const u32 b1 = static_cast<u32>(sm.scal[8]);
   if ((best_key >> 8) == b1) atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
   __syncthreads();
-  if constexpr (COOP) group_histogram<BLOCK>(sm.hist2, g.hist + 256, g.word + 2, tag, Ws);
+  if constexpr (COOP) {
+    group_histogram<BLOCK>(sm.hist2, g.hist + kGroupCopies * 256, sm.stage, g.arrive + W, epoch, w, Ws);
+    TOPK_TRACE(9);
+  }
   if (wid == 0) wave_find_bucket(sm.hist2, need - sm.scal[9], sm.scal + 12, lane);
   __syncthreads();
   const u32 T = (b1 << 8) | static_cast<u32>(sm.scal[12]);
@@ -804,23 +915,21 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
 
   if constexpr (COOP) {
     // ---- 4c. cooperative segment: one candidate list for the whole segment.  Every
-    // workgroup appends its list (an overflowing or threshold-less chunk pushes the count past
-    // the capacity instead), the workgroups meet, and workgroup 0 selects from the list.
-    const u32 contrib = (all_mode || overflow) ? static_cast<u32>(kGroupCap) + 1u : static_cast<u32>(C);
-    if (tid == 0) {
-      sm.scal[6] = static_cast<int>(
-          __hip_atomic_fetch_add(g.count, contrib, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    // workgroup stores its list in its own slot with an epoch-tagged length (an overflowing or
+    // threshold-less chunk stores an oversized length instead), the workgroups meet, and every
+    // workgroup gathers the whole list into LDS.
+    int* cnt = sm.rank;        // [256] list lengths of the segment's workgroups
+    int* pre = sm.rank + 256;  // [256] their exclusive prefix sums
+    const u32 contrib = (all_mode || overflow) ? static_cast<u32>(kCandArea) + 1u : static_cast<u32>(C);
+    u64* mylist = g.lists + static_cast<size_t>(w) * kCandArea;
+    if (contrib <= static_cast<u32>(kCandArea)) {
+      for (u32 i = tid; i < contrib; i += BLOCK) store_agent(mylist + i, sm.area[i]);
     }
-    __syncthreads();
-    u32 base = static_cast<u32>(sm.scal[6]);
-    if (contrib <= static_cast<u32>(kGroupCap) && base + contrib <= static_cast<u32>(kGroupCap)) {
-      for (u32 i = tid; i < contrib; i += BLOCK) {
-        __hip_atomic_store(g.list + base + i, sm.area[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    group_barrier(g.word + 3, tag, Ws);
-    u32 total = __hip_atomic_load(g.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (total > static_cast<u32>(kGroupCap)) {
+    if (tid == 0) store_agent(g.counts + w, (tag << 20) | contrib);
+    group_barrier(g.arrive + 2 * W, epoch, w, Ws);
+    TOPK_TRACE(10);
+    u32 total = group_gather<BLOCK>(g.counts, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20);
+    if (total == kAbsent) {
       // ---- 4d. the list would not fit: exact radix refinement over the whole segment of
       // Q = key16 << 32 | index32 among the elements with key <= T, one global histogram per
       // 8-bit digit, until at most kGroupCap elements are <= the bound.
@@ -836,17 +945,17 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
           if (key <= T && (Q & pmask) == prefix) atomicAdd(&sm.hist[(Q >> shift) & 255u], 1u);
         });
         __syncthreads();
-        group_histogram<BLOCK>(sm.hist, g.hist + (2 + pass) * 256, g.word + 4 + pass, tag, Ws);
+        group_histogram_single<BLOCK>(sm.hist, g.rhist + pass * 256, g.arrive + (3 + pass) * W, epoch, w, Ws);
         if (wid == 0) wave_find_bucket(sm.hist, rneed, sm.scal, lane);
         __syncthreads();
         const int b = sm.scal[0];
         const int before = sm.scal[1];
-        const int cnt = sm.scal[2];
+        const int cnt_b = sm.scal[2];
         __syncthreads();
         rneed -= before;
         prefix |= static_cast<u64>(b) << shift;
         pmask |= 0xffull << shift;
-        if ((kk - rneed) + cnt <= kGroupCap) break;
+        if ((kk - rneed) + cnt_b <= kGroupCap) break;
       }
       const u64 bound = prefix | (~pmask & 0xFFFFFFFFFFFFull);
       if (tid == 0) sm.scal[4] = 0;
@@ -862,27 +971,25 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
       });
       __syncthreads();
       const u32 c2 = static_cast<u32>(sm.scal[4] < kArea ? sm.scal[4] : kArea);
-      if (tid == 0) {
-        sm.scal[6] = static_cast<int>(
-            __hip_atomic_fetch_add(g.count + 1, c2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      }
-      __syncthreads();
-      base = static_cast<u32>(sm.scal[6]);
-      for (u32 i = tid; i < c2; i += BLOCK) {
-        if (base + i < static_cast<u32>(kGroupCap)) {
-          __hip_atomic_store(g.list + base + i, sm.area[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-      group_barrier(g.word + 10, tag, Ws);
-      total = __hip_atomic_load(g.count + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      total = total < static_cast<u32>(kGroupCap) ? total : static_cast<u32>(kGroupCap);
+      for (u32 i = tid; i < c2; i += BLOCK) store_agent(mylist + i, sm.area[i]);
+      if (tid == 0) store_agent(g.counts + W + w, (tag << 20) | c2);
+      group_barrier(g.arrive + 9 * W, epoch, w, Ws);
+      total = group_gather<BLOCK>(g.counts + W, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20);
+      if (total == kAbsent) total = 0;  // cannot happen: at most kGroupCap elements are <= bound
     }
-    if (w != 0) return;
-    for (u32 i = tid; i < total; i += BLOCK) {
-      sm.area[i] = __hip_atomic_load(g.list + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Every workgroup ranks its share of the list; workgroup 0 writes the pads.
+    if (w == 0) {
+      for (int r = kk + tid; r < k; r += BLOCK) {
+        const int64_t o = static_cast<int64_t>(seg) * k + r;
+        p.out_idx[o] = -1;
+        p.out_vals[o] = 0xffffu;
+      }
     }
-    __syncthreads();
-    finalize_segment<BLOCK>(p, sm, static_cast<int>(total), kk, n, seg);
+    const int per = (static_cast<int>(total) + Ws - 1) / Ws;
+    const int c0 = w * per < static_cast<int>(total) ? w * per : static_cast<int>(total);
+    const int c1 = c0 + per < static_cast<int>(total) ? c0 + per : static_cast<int>(total);
+    rank_range_write<BLOCK>(p, n, seg, sm.area, static_cast<int>(total), kk, c0, c1);
+    TOPK_TRACE(11);
     return;
   }
   if (all_mode && nc <= kArea) {
@@ -1010,15 +1117,49 @@ int launch_shape(const Plan& plan, const TopkParams& params, hipStream_t stream)
   return static_cast<int>(hipGetLastError());
 }
 
-// Cooperative launch: the runtime refuses (hipErrorCooperativeLaunchTooLarge) a grid that
-// cannot be co-resident, so the workgroups' barriers always complete.
+// Launch of the cooperative path.  Its workgroups wait for each other, so all of them must be
+// resident at once: one 1024-thread workgroup fits every CU, and the grid is refused
+// (hipErrorCooperativeLaunchTooLarge) when it has more workgroups than the device has CUs.
+// Within that bound an ordinary launch places every workgroup immediately (kernels of other
+// streams only delay the placement; they do not wait for this one), and it costs far less
+// than hipLaunchCooperativeKernel.  BATCH_TOPK_AMD_COOPERATIVE_LAUNCH=1 selects the runtime's
+// cooperative launch, which checks co-residency itself.
+int device_cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+bool formal_cooperative_launch() {
+  static const bool on = [] {
+    const char* e = std::getenv("BATCH_TOPK_AMD_COOPERATIVE_LAUNCH");
+    return e != nullptr && e[0] == '1';
+  }();
+  return on;
+}
+
 int launch_cooperative(const Plan& plan, TopkParams params, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(params.seg_num) * plan.W));
-  void* args[] = {&params};
-  const hipError_t e = hipLaunchCooperativeKernel(
-      reinterpret_cast<const void*>(&segmented_topk_kernel<1024, 16, true>), grid, dim3(1024), args,
-      static_cast<unsigned>(plan.lds_bytes), stream);
-  if (e != hipSuccess) return static_cast<int>(e);
+  const int64_t groups = static_cast<int64_t>(params.seg_num) * plan.W;
+  if (groups > device_cu_count()) return static_cast<int>(hipErrorCooperativeLaunchTooLarge);
+  const dim3 grid(static_cast<unsigned>(groups));
+  if (formal_cooperative_launch()) {
+    void* args[] = {&params};
+    const hipError_t e = hipLaunchCooperativeKernel(
+        reinterpret_cast<const void*>(&segmented_topk_kernel<1024, 16, true>), grid, dim3(1024), args,
+        static_cast<unsigned>(plan.lds_bytes), stream);
+    if (e != hipSuccess) return static_cast<int>(e);
+  } else {
+    hipLaunchKernelGGL((segmented_topk_kernel<1024, 16, true>), grid, dim3(1024),
+                       static_cast<unsigned>(plan.lds_bytes), stream, params);
+  }
   return static_cast<int>(hipGetLastError());
 }
 

@@ -6,12 +6,17 @@ batch (the inputs already resident in HBM).  The input is replicated over >= 512
 distinct buffers and the timed calls rotate through them, so the 256 MB Infinity Cache cannot
 serve the reads; a cache-resident ("warm") timing of a single buffer is reported separately.
 
-Prints ONE JSON line (rank 0):
+Prints ONE JSON line:
   value       = whole-job segments per second over the timed steps;
-  roofline    = algorithmic bytes per launch / median kernel time from HIP events on the
-                launch stream, against the 8 TB/s HBM peak;
+  roofline    = algorithmic bytes per launch (2 B per input element + 6 B per output rank)
+                / the average launch duration over the timed region (HIP events on the launch
+                stream around K back-to-back launches), against the 8 TB/s HBM peak;
+                traffic = HBM bytes per launch measured with rocprofv3 (profiles/traffic.json);
   cpu_baseline= the reference's host verifier (std::stable_sort per segment, restated in
                 oracle/) timed on this host's cores over the whole batch.
+
+Other workloads (--workload uniform_small | ties_special | varlen | huge_segment) print the
+same line for that configuration.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--k K]
 """
@@ -36,20 +41,41 @@ def log(msg: str) -> None:
 
 
 def make_input(name: str):
+    """-> (bits [seg_num, seg_len] or flat for offsets, int32 offsets or None, config dict)."""
     from batch_topk_amd import workloads as wl
 
     if name == "llm_logits":
         bits = wl.llm_logits()
-        return bits, dict(workload="llm_logits: 128x128256 fp16 N(0,sd 2), 0.1% of each row +8",
-                          seg_num=128, seg_len=128256)
+        return bits, None, dict(workload="llm_logits: 128x128256 fp16 N(0,sd 2), 0.1% of each row +8",
+                                seg_num=128, seg_len=128256)
     if name == "uniform_small":
         bits = wl.uniform_small()
-        return bits, dict(workload="uniform_small: 16x4096 fp16 U(-1,1)", seg_num=16, seg_len=4096)
+        return bits, None, dict(workload="uniform_small: 16x4096 fp16 U(-1,1)", seg_num=16, seg_len=4096)
     if name == "ties_special":
         bits = wl.ties_special()
-        return bits, dict(workload="ties_special: 256x32000 fp16, 256 distinct values, 1% -inf, 0.1% NaN",
-                          seg_num=256, seg_len=32000)
+        return bits, None, dict(workload="ties_special: 256x32000 fp16, 256 distinct values, 1% -inf, 0.1% NaN",
+                                seg_num=256, seg_len=32000)
+    if name == "huge_segment":
+        bits = wl.huge_segment()
+        return bits, None, dict(workload="huge_segment: 1x16777216 fp16 N(0,1)", seg_num=1, seg_len=16777216)
+    if name == "varlen":
+        bits, offsets = wl.varlen()
+        return bits, offsets, dict(workload="varlen: 512 segments, lengths U[1,65536], fp16 N(0,1), int32 offsets",
+                                   seg_num=512, max_seg_len=65536, elements=int(offsets[-1]))
     raise SystemExit(f"unknown workload {name}")
+
+
+def load_traffic(workload: str, k: int):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (and scaled by a
+    copy kernel of known size), from the committed summary; None if not measured."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = table.get(f"{workload}:k={k}")
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
 def cpu_baseline(bits: np.ndarray, k: int, threads: int):
@@ -97,15 +123,24 @@ def main() -> int:
 
     bt.load_library()
     dev = torch.device("cuda:0")
-    bits, cfg = make_input(args.workload)
-    seg_num, seg_len = bits.shape
+    bits, offsets, cfg = make_input(args.workload)
     k = args.k
+    if offsets is None:
+        seg_num, seg_len = bits.shape
+        n_elements = seg_num * seg_len
+        ws_bytes = bt.batch_topk_half_workspace_size(seg_num, seg_len, k)
+    else:
+        seg_num, seg_len = offsets.size - 1, int(np.max(np.diff(offsets)))
+        n_elements = int(offsets[-1])
+        ws_bytes = bt.batch_topk_half_segmented_workspace_size(seg_num, cfg["max_seg_len"], k)
+        d_off = torch.from_numpy(offsets.astype(np.int32)).to(dev)
+    if ws_bytes == 0:
+        raise SystemExit(f"shape not supported: {cfg} k={k}")
     in_bytes = bits.nbytes
     copies = max(1, -(-args.rotate_mb * 2**20 // in_bytes))
     log(f"workload {cfg['workload']} k={k}, {copies} input copies ({copies * in_bytes / 2**20:.0f} MB)")
     src = torch.from_numpy(bits.view(np.int16)).to(dev)
     inputs = [src] + [src.clone() for _ in range(copies - 1)]
-    ws_bytes = bt.batch_topk_half_workspace_size(seg_num, seg_len, k)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     vals = torch.empty((seg_num, k), dtype=torch.int16, device=dev)
     idx = torch.empty((seg_num, k), dtype=torch.int32, device=dev)
@@ -113,10 +148,15 @@ def main() -> int:
     sh = stream.cuda_stream
 
     def call(i: int) -> None:
-        rc = bt.batch_topk_half(inputs[i % copies].data_ptr(), seg_num, seg_len, k, vals.data_ptr(),
-                                idx.data_ptr(), ws.data_ptr(), ws_bytes, sh)
+        if offsets is None:
+            rc = bt.batch_topk_half(inputs[i % copies].data_ptr(), seg_num, seg_len, k, vals.data_ptr(),
+                                    idx.data_ptr(), ws.data_ptr(), ws_bytes, sh)
+        else:
+            rc = bt.batch_topk_half_segmented(inputs[i % copies].data_ptr(), d_off.data_ptr(), seg_num,
+                                              cfg["max_seg_len"], k, vals.data_ptr(), idx.data_ptr(),
+                                              ws.data_ptr(), ws_bytes, sh)
         if rc != 0:
-            raise RuntimeError(f"batch_topk_half returned {rc}")
+            raise RuntimeError(f"top-k call returned {rc}")
 
     for i in range(args.warmup):
         call(i)
@@ -127,7 +167,10 @@ def main() -> int:
 
     call(0)
     torch.cuda.synchronize()
-    ev, ei = O.batch_topk_half(bits[:8], k, seg_len=seg_len)
+    if offsets is None:
+        ev, ei = O.batch_topk_half(bits[:8], k, seg_len=seg_len)
+    else:
+        ev, ei = O.batch_topk_half(bits[:int(offsets[8])], k, offsets=offsets[:9].astype(np.int64))
     gi = idx.cpu().numpy()[:8]
     gv = vals.cpu().numpy().view(np.uint16)[:8]
     parity_ok = bool(np.array_equal(gi, ei) and np.array_equal(gv, ev))
@@ -161,11 +204,18 @@ def main() -> int:
     warm_us = per_launch(100, False)
     kern_us = float(np.median(cold_us))
 
-    alg_bytes = 2 * seg_num * seg_len + 6 * seg_num * k
-    achieved = alg_bytes / (kern_us * 1e-6)
+    # Algorithmic bytes: every input element read once (2 B), every output rank written once
+    # (2 B value + 4 B index), plus the offsets array when given.
+    alg_bytes = 2 * n_elements + 6 * seg_num * k + (0 if offsets is None else 4 * (seg_num + 1))
+    # The kernel's average launch duration over the timed region (back-to-back launches,
+    # events on the launch stream).
+    step_us = ms_per_step * 1e3
+    achieved = alg_bytes / (step_us * 1e-6)
     value = seg_num * steps / (total_ms * 1e-3)
+    metric = METRIC if (args.workload == "llm_logits" and k == 50) else \
+        f"segments/s and achieved HBM GB/s, fp16 top-{k} over {cfg['workload'].split(':')[0]}"
     result = {
-        "metric": METRIC,
+        "metric": metric,
         "value": value,
         "unit": "segments/s",
         "n_gpus": 1,
@@ -184,17 +234,17 @@ def main() -> int:
             "peak": HBM_PEAK_BPS / 1e9,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_BPS,
-            "traffic": None,
+            "traffic": load_traffic(args.workload, k),
         },
-        "elements_per_s": seg_num * seg_len * steps / (total_ms * 1e-3),
+        "elements_per_s": n_elements * steps / (total_ms * 1e-3),
         "hbm_gbps_whole_job": alg_bytes * steps / (total_ms * 1e-3) / 1e9,
-        "kernel_us_median": kern_us,
+        "kernel_us_isolated_median": kern_us,
         "kernel_us_p10_p90": [float(np.percentile(cold_us, 10)), float(np.percentile(cold_us, 90))],
-        "warm_kernel_us_median": float(np.median(warm_us)),
+        "warm_kernel_us_isolated_median": float(np.median(warm_us)),
         "alg_bytes_per_launch": alg_bytes,
         "parity_spot_check": parity_ok,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and offsets is None:
         log("timing the CPU baseline (reference host verifier)...")
         t0 = time.time()
         result["cpu_baseline"] = cpu_baseline(bits, k, args.cpu_threads)
