@@ -16,7 +16,9 @@
  *
  * Return values are hipError_t codes as int: 0 = hipSuccess; 1 = hipErrorInvalidValue
  * for any rejected argument, returned before any HIP call is made; otherwise the HIP
- * error of the failed launch.
+ * error of the failed launch.  Long segments with large k run as one cooperative grid
+ * whose workgroups must all be resident at once (one per CU); a shape that needs more
+ * workgroups than the device has CUs returns hipErrorCooperativeLaunchTooLarge.
  *
  * The workspace is owned by the caller, its content on entry may be arbitrary, and it
  * must not be shared by calls that can run concurrently.
@@ -51,8 +53,7 @@ int radix_topk_batch_topk_half(const uint16_t* d_input, int seg_num, int seg_len
 /*
  * Workspace bytes for radix_topk_batch_topk_half; 0 for an unsupported shape.
  * Replaces radix_topk::batch_topk_half_workspace_size (reference include/batch_topk.cuh:21,
- * src/batch_topk.cu:35-40).  Depends only on the shape (and on the device's CU count,
- * which is queried once), never on the data.
+ * src/batch_topk.cu:35-40).  Depends only on the shape, never on the data or the device.
  */
 size_t radix_topk_batch_topk_half_workspace_size(int seg_num, int seg_len, int k);
 
