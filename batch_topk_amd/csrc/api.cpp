@@ -21,6 +21,9 @@ namespace {
 
 constexpr int kMaxK = RADIX_TOPK_MAX_K;
 constexpr size_t kAlign = 256;
+// CU count the plan assumes (MI355X).  The plan depends on the shape only; the device's own
+// CU count is checked at launch where it matters (the cooperative path).
+constexpr int kPlanCUs = 256;
 constexpr int kInvalid = static_cast<int>(hipErrorInvalidValue);
 
 int next_pow2(int x) {
@@ -34,9 +37,8 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // Launch plan for segments of at most `max_len` elements (plus up to 7 elements of
 // misalignment of the 16-byte load grid), `seg_num` segments and `k` outputs each.
 //
-// A segment that fits one workgroup (<= kMaxChunk elements) gets exactly one, of the smallest
-// shape (vectors per thread first, then threads) that covers it, with at least 4k threads so
-// each wave's share of k stays well below its 64 lanes.  Longer segments are split into
+// The workgroup shape has at least 4k threads so each wave's share of k stays well below its
+// 64 lanes; the rest of the choice depends on how many segments share a CU (below).  Longer segments are split into
 // kMaxChunk chunks whose candidate lists are merged by the last workgroup to finish, while
 // the W lists fit one workgroup's LDS merge area.  Beyond that (long segments with large k)
 // the segment's W workgroups run cooperatively: all co-resident, they build one
@@ -49,15 +51,32 @@ Plan make_plan(int seg_num, int64_t max_len, int k) {
   const int64_t span = max_len + 7;  // worst-case aligned span of one segment
   int block = 1024, vpt = 16;
   bool found = false;
-  for (int cv : {2, 4, 8, 16}) {
+  if (seg_num >= 2 * kPlanCUs) {
+    // More segments than two per CU: the fewest threads whose chunk covers max_len, so that
+    // several workgroups share a CU and one's loads overlap another's selection.  A segment
+    // whose misaligned span reaches past the chunk takes a second (tail) workgroup.
     for (int cb = block_min; cb <= 1024 && !found; cb *= 2) {
-      if (static_cast<int64_t>(cb) * cv * 8 >= span) {
-        block = cb;
-        vpt = cv;
-        found = true;
+      for (int cv : {2, 4, 8, 16}) {
+        if (!found && static_cast<int64_t>(cb) * cv * 8 >= max_len) {
+          block = cb;
+          vpt = cv;
+          found = true;
+        }
       }
     }
-    if (found) break;
+  } else {
+    // Up to two segments per CU: one workgroup per segment with the fewest vectors per
+    // thread (then the fewest threads) that covers the whole aligned span.
+    for (int cv : {2, 4, 8, 16}) {
+      for (int cb = block_min; cb <= 1024 && !found; cb *= 2) {
+        if (static_cast<int64_t>(cb) * cv * 8 >= span) {
+          block = cb;
+          vpt = cv;
+          found = true;
+        }
+      }
+      if (found) break;
+    }
   }
   const int chunk = block * vpt * 8;
   const int64_t W = span <= chunk ? 1 : (span + chunk - 1) / chunk;

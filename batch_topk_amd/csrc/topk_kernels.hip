@@ -609,8 +609,10 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   const int lane = tid & 63;
   const int wid = tid >> 6;
   const int W = p.chunks_per_seg;
-  const int seg = static_cast<int>(blockIdx.x) / W;
-  const int w = static_cast<int>(blockIdx.x) - seg * W;
+  // Chunk-major grid: every segment's first chunk is dispatched before any second chunk, so
+  // the workgroups of chunks a segment does not reach (they return at once) come last.
+  const int w = static_cast<int>(blockIdx.x) / p.seg_num;
+  const int seg = static_cast<int>(blockIdx.x) - w * p.seg_num;
   const int k = p.k;
 
   int64_t s0, s1;

@@ -12,6 +12,12 @@ The five workloads the engine is measured and checked on:
                        0x7E00, 0xFE00, 0x7C01, 0xFFFF in turn), k in {1, 16, 128, 256}.
 * ``huge_segment``     1 x 16,777,216, N(0, 1), k = 1024.
 
+And the reference's own benchmark matrix (``ref_matrix``): seg_num in {128, 1500, 3000, 4500,
+6000} x 10000, k = 50, filled as the reference's bench fills its input
+(bench/bench_batch_topk.cu:9-15: element i = ((i * 17 + 13) mod 2048 - 1024) / 16 over the
+whole batch, exact in fp16), with the reference's RTX 4080 targets
+(include/batch_topk_benchmark.cuh:14-20).
+
 Every generator returns raw fp16 bit patterns (uint16) so that NaN payloads and the sign of
 zero survive; float -> fp16 conversion is numpy's round-to-nearest-even cast.
 """
@@ -80,10 +86,27 @@ def huge_segment(seed: int = 0, n: int = 16_777_216):
     return _f16_bits(rng.standard_normal((1, n), dtype=np.float32))
 
 
+# (seg_num, seg_len, k) -> target latency in us on RTX 4080 (include/batch_topk_benchmark.cuh:14-20)
+REF_MATRIX_TARGET_US = {
+    (128, 10000, 50): 11.0,
+    (1500, 10000, 50): 82.0,
+    (3000, 10000, 50): 161.0,
+    (4500, 10000, 50): 241.0,
+    (6000, 10000, 50): 319.0,
+}
+
+
+def ref_matrix(seg_num: int = 128, seg_len: int = 10000):
+    i = np.arange(seg_num * seg_len, dtype=np.int64)
+    raw = (i * 17 + 13) % 2048 - 1024
+    return _f16_bits((raw.astype(np.float32) / np.float32(16.0)).reshape(seg_num, seg_len))
+
+
 WORKLOADS = {
     "uniform_small": dict(gen=uniform_small, k=(50,)),
     "llm_logits": dict(gen=llm_logits, k=(50,)),
     "varlen": dict(gen=varlen, k=(64,)),
     "ties_special": dict(gen=ties_special, k=(1, 16, 128, 256)),
     "huge_segment": dict(gen=huge_segment, k=(1024,)),
+    "ref_matrix": dict(gen=ref_matrix, k=(50,)),
 }

@@ -15,8 +15,9 @@ Prints ONE JSON line:
   cpu_baseline= the reference's host verifier (std::stable_sort per segment, restated in
                 oracle/) timed on this host's cores over the whole batch.
 
-Other workloads (--workload uniform_small | ties_special | varlen | huge_segment) print the
-same line for that configuration.
+Other workloads (--workload uniform_small | ties_special | varlen | huge_segment, and
+ref_matrix --seg-num N for the reference's own benchmark matrix) print the same line for
+that configuration.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--k K]
 """
@@ -40,9 +41,15 @@ def log(msg: str) -> None:
     sys.stderr.flush()
 
 
-def make_input(name: str):
+def make_input(name: str, seg_num_arg: int | None = None):
     """-> (bits [seg_num, seg_len] or flat for offsets, int32 offsets or None, config dict)."""
     from batch_topk_amd import workloads as wl
+
+    if name == "ref_matrix":
+        n = seg_num_arg or 128
+        bits = wl.ref_matrix(n)
+        return bits, None, dict(workload=f"ref_matrix: {n}x10000 fp16, the reference bench's fill pattern",
+                                seg_num=n, seg_len=10000)
 
     if name == "llm_logits":
         bits = wl.llm_logits()
@@ -108,6 +115,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="llm_logits")
     ap.add_argument("--k", type=int, default=50)
+    ap.add_argument("--seg-num", type=int, default=None, help="segments of the ref_matrix workload")
     ap.add_argument("--rotate-mb", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
@@ -123,7 +131,7 @@ def main() -> int:
 
     bt.load_library()
     dev = torch.device("cuda:0")
-    bits, offsets, cfg = make_input(args.workload)
+    bits, offsets, cfg = make_input(args.workload, args.seg_num)
     k = args.k
     if offsets is None:
         seg_num, seg_len = bits.shape
@@ -244,6 +252,12 @@ def main() -> int:
         "alg_bytes_per_launch": alg_bytes,
         "parity_spot_check": parity_ok,
     }
+    if args.workload == "ref_matrix":
+        from batch_topk_amd.workloads import REF_MATRIX_TARGET_US
+
+        target = REF_MATRIX_TARGET_US.get((seg_num, seg_len, k))
+        result["reference_target_us_rtx4080"] = target
+        result["target_over_measured"] = None if target is None else target / (ms_per_step * 1e3)
     if not args.no_cpu_baseline and offsets is None:
         log("timing the CPU baseline (reference host verifier)...")
         t0 = time.time()

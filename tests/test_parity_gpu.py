@@ -246,3 +246,36 @@ def test_cooperative_variable_segments():
     got = run_segmented(bits, offsets, 300, 400_000, poison=0x5A)
     exp = O.batch_topk_half(bits, 300, offsets=offsets.astype(np.int64), threads=THREADS)
     assert_same(got, exp, "cooperative varlen")
+
+
+# ------------------------------------------------------------------ the reference's benchmark matrix
+
+@pytest.mark.parametrize("seg_num", [128, 1500, 6000])
+def test_reference_benchmark_matrix(seg_num):
+    # bench/bench_batch_topk.cu:9-15 fill pattern at the shapes of
+    # include/batch_topk_benchmark.cuh:14-20 (heavy ties: 2048 distinct values per period)
+    bits = wl.ref_matrix(seg_num)
+    check_fixed(bits, 50, f"reference bench matrix {seg_num}x10000")
+
+
+# ------------------------------------------------------------------ many segments, tail chunks
+# With at least two segments per CU the plan takes the smallest workgroup covering max_len;
+# a segment whose misaligned span reaches past that chunk gets a second (tail) workgroup.
+
+def test_many_segments_with_tail_chunks():
+    rng = np.random.default_rng(41)
+    lengths = rng.integers(1, 300, size=600).astype(np.int64)
+    lengths[[3, 100, 333, 599]] = [65536, 65533, 65530, 65536]
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    bits = rng.standard_normal(int(offsets[-1])).astype(np.float16).view(np.uint16)
+    for k, elem_offset in ((64, 3), (1, 7), (64, 0)):
+        announce(f"many segments with tail chunks k={k} offset={elem_offset}")
+        got = run_segmented(bits, offsets, k, 65536, elem_offset=elem_offset, poison=0x3C)
+        exp = O.batch_topk_half(bits, k, offsets=offsets.astype(np.int64), threads=THREADS)
+        assert_same(got, exp, f"tail chunks k={k}")
+
+
+def test_fixed_length_tail_chunks():
+    rng = np.random.default_rng(43)
+    bits = rng.standard_normal((512, 16384)).astype(np.float16).view(np.uint16)
+    check_fixed(bits, 50, "512x16384 misaligned", elem_offset=3)
