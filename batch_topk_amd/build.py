@@ -48,5 +48,34 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
+def resource_usage() -> dict:
+    """Per-kernel VGPRs, scratch bytes per lane and occupancy (waves per SIMD) of the device
+    code, from the compiler's kernel-resource-usage remarks (device-only compile)."""
+    cmd = [hipcc(), *HIP_FLAGS, "--cuda-device-only", "-c", "-o", os.devnull,
+           "-Rpass-analysis=kernel-resource-usage", os.path.join(CSRC, "topk_kernels.hip")]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed on the resource-usage compile")
+    out: dict = {}
+    name = None
+    for line in res.stderr.splitlines():
+        if "remark:" not in line:
+            continue
+        text = line.split("remark:", 1)[1].strip()
+        text = text.replace("[-Rpass-analysis=kernel-resource-usage]", "").strip()
+        if text.startswith("Function Name:"):
+            name = text.split(":", 1)[1].strip()
+            out[name] = {}
+        elif name is not None and ":" in text:
+            key, val = text.split(":", 1)
+            val = val.strip()
+            try:
+                out[name][key.strip()] = int(val)
+            except ValueError:
+                out[name][key.strip()] = val
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose=True))

@@ -594,8 +594,11 @@ __device__ __forceinline__ u32 vec_min2(const uint4& x) {
 
 // ------------------------------------------------------------------------------ the kernel
 
+// At least 4 waves per SIMD (at most 128 VGPRs): one 1024-thread workgroup, or two 512-thread
+// ones, per CU.
 template <int BLOCK, int VPT, bool COOP>
-__global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
+__global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
+segmented_topk_kernel(TopkParams p) {
   constexpr int NW = BLOCK / 64;
   constexpr int CH = BLOCK * VPT * 8;
   constexpr int JT = VPT;  // vectors the threshold is computed from
@@ -611,8 +614,8 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   const int W = p.chunks_per_seg;
   // Chunk-major grid: every segment's first chunk is dispatched before any second chunk, so
   // the workgroups of chunks a segment does not reach (they return at once) come last.
-  const int w = static_cast<int>(blockIdx.x) / p.seg_num;
-  const int seg = static_cast<int>(blockIdx.x) - w * p.seg_num;
+  const int w = W == 1 ? 0 : static_cast<int>(blockIdx.x) / p.seg_num;
+  const int seg = W == 1 ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) - w * p.seg_num;
   const int k = p.k;
 
   int64_t s0, s1;
@@ -678,11 +681,13 @@ __global__ void __launch_bounds__(BLOCK) segmented_topk_kernel(TopkParams p) {
   uint4 v[VPT];
   const unsigned char* cptr = reinterpret_cast<const unsigned char*>(p.base + cb);
   const u32 lo_blk = static_cast<u32>(lo & ~7);
+  const u32 any_lo = static_cast<u32>(lo - 7);             // a block holds an element of [lo, hi)
+  const u32 any_span = static_cast<u32>(hi) - any_lo;      // iff pos - (lo - 7) < hi - (lo - 7)
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int pos = (j * BLOCK + tid) * 8;
-    const bool any = pos < hi && pos + 8 > lo;
-    v[j] = load_nt(cptr, (any ? static_cast<u32>(pos) : lo_blk) * 2u);
+    const u32 pos = static_cast<u32>((j * BLOCK + tid) * 8);
+    const bool any = pos - any_lo < any_span;
+    v[j] = load_nt(cptr, (any ? pos : lo_blk) * 2u);
   }
   for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
   __syncthreads();  // histogram cleared (the loads stay in flight)

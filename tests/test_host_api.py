@@ -113,3 +113,17 @@ def test_torch_helpers_fail_loudly_without_gpu():
     x = torch.zeros((2, 8), dtype=torch.float16)
     with pytest.raises(ValueError):
         bt.topk(x, 3)   # CPU tensor: there is no CPU fallback
+
+
+def test_kernel_resources_keep_occupancy_without_spills():
+    # Every instantiation must run at least 4 waves per SIMD (one 1024-thread or two
+    # 512-thread workgroups per CU) with no scratch spills: the kernels are latency-bound,
+    # and a lost workgroup slot or a spill shows up directly in the per-call time.
+    from batch_topk_amd.build import resource_usage
+
+    usage = resource_usage()
+    kernels = {k: v for k, v in usage.items() if "segmented_topk_kernel" in k}
+    assert len(kernels) == 13, sorted(kernels)
+    for name, r in kernels.items():
+        assert r["ScratchSize [bytes/lane]"] == 0, (name, r)
+        assert r["Occupancy [waves/SIMD]"] >= 4, (name, r)
