@@ -27,7 +27,10 @@ constexpr int kMaxChunk = 1024 * 16 * 8;
 //   lists   u64 [W][kCandArea]        every workgroup's candidate list
 constexpr int kGroupBarriers = 10;
 constexpr int kGroupCopies = 16;
-constexpr int kGroupCap = kCandArea;  // longest whole-segment list the final ranking takes
+// Longest whole-segment list the final ranking takes: it is gathered into the LDS from the
+// candidate area onward (area, selection, rank and staging regions, free by then), which
+// holds at least 6464 entries for every k.
+constexpr int kGroupCap = 6144;
 struct GroupLayout {
   size_t flag, arrive, counts, hist, rhist, lists, bytes;
 };

@@ -511,18 +511,25 @@ __device__ void group_histogram_single(u32* lds_hist, u32* ghist, u64* slots, u6
   __syncthreads();
 }
 
-// Whole-segment candidate list from the workgroups' lists: reads the W tagged lengths,
-// prefix-sums them (wave 0), and, if no list overflowed and the total fits kGroupCap, gathers
-// every entry into `area`.  Returns the total, or kAbsent when the list cannot be formed.
+// Whole-segment candidate list from the workgroups' lists.  Each workgroup has stored its
+// list and then, as its arrival, its epoch-tagged length: threads 0..arrivals-1 each wait for
+// one length (no separate barrier), wave 0 prefix-sums them, and if no list overflowed and
+// the total fits kGroupCap every entry is gathered into `area`.  Returns the total, or
+// kAbsent when the list cannot be formed.  `cnt` and `pre` are 256-int LDS arrays.
 template <int BLOCK>
-__device__ u32 group_gather(const u64* counts, const u64* lists, u64 tag, int arrivals, u64* area,
-                            int* cnt, int* pre, int* scal) {
+__device__ u32 group_collect(const u64* counts, const u64* lists, u64 tag, int arrivals, u64* area,
+                             int* cnt, int* pre, int* scal) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   if (tid < 256) {
     u32 c = 0;
     if (tid < arrivals) {
-      c = tagged_value(load_agent(counts + tid), tag);
+      c = kAbsent;
+      for (u32 spin = 0; spin < kGroupSpinLimit; ++spin) {
+        c = tagged_value(load_agent(counts + tid), tag);
+        if (c != kAbsent) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
       if (c > static_cast<u32>(kCandArea)) c = static_cast<u32>(kGroupCap) + 1u;  // overflow or absent
     }
     cnt[tid] = static_cast<int>(c);
@@ -542,13 +549,33 @@ __device__ u32 group_gather(const u64* counts, const u64* lists, u64 tag, int ar
   __syncthreads();
   const u32 total = static_cast<u32>(scal[0]);
   if (total > static_cast<u32>(kGroupCap)) return kAbsent;
-  for (u32 i = tid; i < total; i += BLOCK) {
+  // All of a thread's entries are located first and then loaded together, so their latencies
+  // overlap.
+  constexpr int kPer = (kGroupCap + BLOCK - 1) / BLOCK;
+  const int rounds = static_cast<int>((total + BLOCK - 1) / BLOCK);  // workgroup-uniform
+  size_t src[kPer];
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    src[r] = 0;
+    if (r >= rounds) continue;
+    const u32 i = static_cast<u32>(tid + r * BLOCK);
     int lo_t = 0, hi_t = arrivals;  // last t with pre[t] <= i
     while (hi_t - lo_t > 1) {
       const int mid = (lo_t + hi_t) >> 1;
       if (static_cast<u32>(pre[mid]) <= i) lo_t = mid; else hi_t = mid;
     }
-    area[i] = load_agent(lists + static_cast<size_t>(lo_t) * kCandArea + (i - static_cast<u32>(pre[lo_t])));
+    src[r] = static_cast<size_t>(lo_t) * kCandArea + (i - static_cast<u32>(pre[lo_t]));
+  }
+  u64 val[kPer];
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const u32 i = static_cast<u32>(tid + r * BLOCK);
+    val[r] = i < total ? load_agent(lists + src[r]) : 0ull;
+  }
+#pragma unroll
+  for (int r = 0; r < kPer; ++r) {
+    const u32 i = static_cast<u32>(tid + r * BLOCK);
+    if (i < total) area[i] = val[r];
   }
   __syncthreads();
   return total;
@@ -744,6 +771,8 @@ segmented_topk_kernel(TopkParams p) {
   if ((best_key >> 8) == b1) atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
   __syncthreads();
   if constexpr (COOP) {
+    // Whole segment: an exact second byte as well (a coarse bucket bound would save this round
+    // of cross-workgroup latency but quadruple the list the final ranking has to sort).
     group_histogram<BLOCK>(sm.hist2, g.hist + kGroupCopies * 256, sm.stage, g.arrive + W, epoch, w, Ws);
     TOPK_TRACE(9);
   }
@@ -925,21 +954,23 @@ segmented_topk_kernel(TopkParams p) {
     // workgroup stores its list in its own slot with an epoch-tagged length (an overflowing or
     // threshold-less chunk stores an oversized length instead), the workgroups meet, and every
     // workgroup gathers the whole list into LDS.
-    int* cnt = sm.rank;        // [256] list lengths of the segment's workgroups
-    int* pre = sm.rank + 256;  // [256] their exclusive prefix sums
+    int* cnt = reinterpret_cast<int*>(sm.hist);   // [256] list lengths of the workgroups
+    int* pre = reinterpret_cast<int*>(sm.hist2);  // [256] their exclusive prefix sums
     const u32 contrib = (all_mode || overflow) ? static_cast<u32>(kCandArea) + 1u : static_cast<u32>(C);
     u64* mylist = g.lists + static_cast<size_t>(w) * kCandArea;
     if (contrib <= static_cast<u32>(kCandArea)) {
       for (u32 i = tid; i < contrib; i += BLOCK) store_agent(mylist + i, sm.area[i]);
     }
+    wait_vector_memory();  // the list is complete before its length announces it
+    __syncthreads();
     if (tid == 0) store_agent(g.counts + w, (tag << 20) | contrib);
-    group_barrier(g.arrive + 2 * W, epoch, w, Ws);
     TOPK_TRACE(10);
-    u32 total = group_gather<BLOCK>(g.counts, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20);
+    u32 total = group_collect<BLOCK>(g.counts, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20);
     if (total == kAbsent) {
       // ---- 4d. the list would not fit: exact radix refinement over the whole segment of
       // Q = key16 << 32 | index32 among the elements with key <= T, one global histogram per
-      // 8-bit digit, until at most kGroupCap elements are <= the bound.
+      // 8-bit digit, until at most kCandArea elements are <= the bound (so that any one
+      // workgroup's share fits its own list).
       u64 prefix = 0, pmask = 0;
       int rneed = kk;
       int pass = 0;
@@ -962,7 +993,7 @@ segmented_topk_kernel(TopkParams p) {
         rneed -= before;
         prefix |= static_cast<u64>(b) << shift;
         pmask |= 0xffull << shift;
-        if ((kk - rneed) + cnt_b <= kGroupCap) break;
+        if ((kk - rneed) + cnt_b <= kCandArea) break;  // fits every workgroup's own list
       }
       const u64 bound = prefix | (~pmask & 0xFFFFFFFFFFFFull);
       if (tid == 0) sm.scal[4] = 0;
@@ -979,10 +1010,11 @@ segmented_topk_kernel(TopkParams p) {
       __syncthreads();
       const u32 c2 = static_cast<u32>(sm.scal[4] < kArea ? sm.scal[4] : kArea);
       for (u32 i = tid; i < c2; i += BLOCK) store_agent(mylist + i, sm.area[i]);
+      wait_vector_memory();
+      __syncthreads();
       if (tid == 0) store_agent(g.counts + W + w, (tag << 20) | c2);
-      group_barrier(g.arrive + 9 * W, epoch, w, Ws);
-      total = group_gather<BLOCK>(g.counts + W, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20);
-      if (total == kAbsent) total = 0;  // cannot happen: at most kGroupCap elements are <= bound
+      total = group_collect<BLOCK>(g.counts + W, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20);
+      if (total == kAbsent) total = 0;  // cannot happen: at most kCandArea elements are <= bound
     }
     // Every workgroup ranks its share of the list; workgroup 0 writes the pads.
     if (w == 0) {
