@@ -71,7 +71,6 @@ typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 // 32 words held in registers and read at a wave-uniform index (s_set_gpr_idx), so a loop over
 // a data-dependent set of a lane's vectors compiles to one short body instead of one per vector.
 typedef unsigned u32x32_t __attribute__((ext_vector_type(32)));
-typedef int i32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr u32 kFillWord = 0xFFFFFFFFu;  // two negative NaNs: never a candidate, never a best
 constexpr int kArea = kCandArea;        // LDS candidate entries (candidate list, merged lists)
@@ -622,7 +621,7 @@ __device__ __forceinline__ u32 vec_min2(const uint4& x) {
 // ------------------------------------------------------------------------------ the kernel
 
 // At least 4 waves per SIMD (at most 128 VGPRs): one 1024-thread workgroup, or two 512-thread
-// ones, per CU.
+// ones, per CU.  (Fewer, fatter waves -- 512 threads x 32 vectors -- measured slower.)
 template <int BLOCK, int VPT, bool COOP>
 __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
 segmented_topk_kernel(TopkParams p) {
@@ -733,7 +732,7 @@ segmented_topk_kernel(TopkParams p) {
   }
 
   // ---- 2. thread best over the first JT vectors (packed int16 max / min trees)
-  i32x16_t gm;  // per-vector int16 max of the 8 halves, kept for the filter's vector test
+  int gm[JT];  // per-vector int16 max of the 8 halves, kept for the filter's vector test
   short2_t mx = {static_cast<short>(-32768), static_cast<short>(-32768)};
   short2_t mn = {32767, 32767};
 #pragma unroll
@@ -851,10 +850,11 @@ segmented_topk_kernel(TopkParams p) {
     };
     // Stage the passing vectors: a loop over the wave's passing vector indices, reading the
     // vector at a uniform register index.
-    u32x32_t va, vb;
+    constexpr int NG = (VPT + 7) / 8;  // groups of 8 vectors
+    u32x32_t vv[NG];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      u32x32_t& dst = j < 8 ? va : vb;
+      u32x32_t& dst = vv[j >> 3];
       const int b = (j & 7) * 4;
       dst[b] = v[j].x;
       dst[b + 1] = v[j].y;
@@ -877,8 +877,8 @@ segmented_topk_kernel(TopkParams p) {
         nst += c;
       }
     };
-    stage(va, hv & 0xffu, 0);
-    if constexpr (VPT > 8) stage(vb, hv >> 8, 8);
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) stage(vv[gi], (hv >> (8 * gi)) & 0xffu, 8 * gi);
     TOPK_WTRACE(3);
     if (nst) flush();
     TOPK_WTRACE(4);
