@@ -52,10 +52,11 @@ Plan make_plan(int seg_num, int64_t max_len, int k) {
   int block = 1024, vpt = 16;
   bool found = false;
   if (seg_num >= 2 * kPlanCUs) {
-    // More segments than two per CU: the fewest threads whose chunk covers max_len, so that
-    // several workgroups share a CU and one's loads overlap another's selection.  A segment
+    // More segments than two per CU: the fewest threads (at least 512) whose chunk covers
+    // max_len, so that several workgroups share a CU and one's loads overlap another's
+    // selection.  A segment
     // whose misaligned span reaches past the chunk takes a second (tail) workgroup.
-    for (int cb = block_min; cb <= 1024 && !found; cb *= 2) {
+    for (int cb = block_min > 512 ? block_min : 512; cb <= 1024 && !found; cb *= 2) {
       for (int cv : {2, 4, 8, 16}) {
         if (!found && static_cast<int64_t>(cb) * cv * 8 >= max_len) {
           block = cb;
