@@ -311,6 +311,7 @@ __device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u
   const int mine_i = wid + NW * lane;
   const u64 mine = (lane < PER && mine_i < M) ? list[mine_i] : ~0ull;
   const int count = M > wid ? (M - wid + NW - 1) / NW : 0;
+  TOPK_WTRACE(6);
   int my_rank = kk;
   for (int t = 0; t < count; ++t) {
     const u32 xl = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(mine)), t));
@@ -323,6 +324,7 @@ __device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u
     }
     my_rank = lane == t ? r : my_rank;
   }
+  TOPK_WTRACE(7);
   if (lane < count && my_rank < kk) write_rank(p, n, seg, my_rank, mine);
 }
 
@@ -746,6 +748,7 @@ segmented_topk_kernel(TopkParams p) {
   const int m2 = mn.x < mn.y ? mn.x : mn.y;
   const u32 best_key = desc_key(static_cast<u32>(m1 >= 0 ? m1 : m2) & 0xffffu);
   TOPK_TRACE(1);
+  TOPK_WTRACE(1);
 
   // ---- 3. threshold T = kc-th smallest thread best, by two histogram passes
   atomicAdd(&sm.hist[best_key >> 8], 1u);

@@ -279,3 +279,58 @@ def test_fixed_length_tail_chunks():
     rng = np.random.default_rng(43)
     bits = rng.standard_normal((512, 16384)).astype(np.float16).view(np.uint16)
     check_fixed(bits, 50, "512x16384 misaligned", elem_offset=3)
+
+
+# ------------------------------------------------------------------ seeded random shapes
+# Shape, k, distribution, alignment and entry point drawn from a fixed seed: every plan
+# branch (block/vector shapes, tail chunks, multi-chunk merge, cooperative) meets random data.
+
+def _random_bits(rng, n):
+    kind = rng.integers(0, 6)
+    if kind == 0:
+        x = rng.standard_normal(n).astype(np.float16)
+    elif kind == 1:
+        x = (rng.integers(-8, 9, size=n) * 0.5).astype(np.float16)      # heavy ties
+    elif kind == 2:
+        x = rng.uniform(-1, 1, size=n).astype(np.float16)
+    elif kind == 3:
+        x = np.sort(rng.standard_normal(n)).astype(np.float16)          # sorted
+    elif kind == 4:
+        x = rng.standard_normal(n).astype(np.float16)
+        x[rng.integers(0, n, size=max(1, n // 50))] = np.float16(np.inf)
+        x[rng.integers(0, n, size=max(1, n // 50))] = np.float16(-np.inf)
+    else:
+        return rng.integers(0, 65536, size=n).astype(np.uint16)         # any bit pattern
+    return x.view(np.uint16)
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_fixed_shapes(case):
+    rng = np.random.default_rng(1000 + case)
+    seg_len = int(rng.choice([1, 7, 100, 1000, 4096, 9999, 33000, 70000, 131072, 200000, 400001]))
+    seg_num = int(rng.integers(1, max(2, min(600, 3_000_000 // seg_len))))
+    k = int(min(seg_len, rng.choice([1, 2, 17, 50, 64, 100, 128, 200, 256, 513, 1024])))
+    bits = _random_bits(rng, seg_num * seg_len).reshape(seg_num, seg_len)
+    elem_offset = int(rng.integers(0, 8))
+    check_fixed(bits, k, f"random fixed case {case}", elem_offset=elem_offset)
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_random_segmented_shapes(case):
+    rng = np.random.default_rng(2000 + case)
+    seg_num = int(rng.integers(1, 700))
+    max_len = int(rng.choice([10, 1000, 65536, 131072, 300000]))
+    lengths = rng.integers(0, max_len + 1, size=seg_num).astype(np.int64)
+    while lengths.sum() > 6_000_000:
+        lengths //= 2
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    k = int(rng.choice([1, 16, 50, 64, 128, 300, 1024]))
+    if bt.batch_topk_half_segmented_workspace_size(seg_num, max_len, k) == 0:
+        # beyond the cooperative grid limit (segments x chunks > 256 workgroups)
+        pytest.skip(f"unsupported shape seg_num={seg_num} max_len={max_len} k={k}")
+    bits = _random_bits(rng, max(1, int(offsets[-1])))
+    elem_offset = int(rng.integers(0, 8))
+    announce(f"random segmented case {case}: seg_num={seg_num} max_len={max_len} k={k}")
+    got = run_segmented(bits, offsets, k, max_len, elem_offset=elem_offset, poison=0x77)
+    exp = O.batch_topk_half(bits, k, offsets=offsets.astype(np.int64), threads=THREADS)
+    assert_same(got, exp, f"random segmented case {case}")
