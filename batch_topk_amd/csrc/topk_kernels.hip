@@ -629,7 +629,6 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
 segmented_topk_kernel(TopkParams p) {
   constexpr int NW = BLOCK / 64;
   constexpr int CH = BLOCK * VPT * 8;
-  constexpr int JT = VPT;  // vectors the threshold is computed from
   static_assert(CH <= 65536 * 2, "chunk positions must fit the refinement packing");
   static_assert(NW <= 16, "at most 16 waves");
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -733,19 +732,24 @@ segmented_topk_kernel(TopkParams p) {
     }
   }
 
-  // ---- 2. thread best over the first JT vectors (packed int16 max / min trees)
-  int gm[JT];  // per-vector int16 max of the 8 halves, kept for the filter's vector test
-  short2_t mx = {static_cast<short>(-32768), static_cast<short>(-32768)};
-  short2_t mn = {32767, 32767};
+  // ---- 2. thread best (packed int16 max tree).  As int16, the non-negative-sign halves
+  // order like their values, so the int16 max is the thread's best unless it has none: then
+  // its best is the int16 min (the negative value nearest zero), and only a wave holding such
+  // a lane builds the min tree.  Every VALU instruction here costs all 4 waves of the SIMD.
+  short2_t gv[VPT];  // per-vector packed max, kept for the filter's vector test
 #pragma unroll
-  for (int j = 0; j < JT; ++j) {
-    const short2_t g = as_s2(vec_max2(v[j]));
-    gm[j] = g.x > g.y ? g.x : g.y;
-    mx = __builtin_elementwise_max(mx, g);
-    mn = __builtin_elementwise_min(mn, as_s2(vec_min2(v[j])));
-  }
+  for (int j = 0; j < VPT; ++j) gv[j] = as_s2(vec_max2(v[j]));
+  short2_t mx = gv[0];
+#pragma unroll
+  for (int j = 1; j < VPT; ++j) mx = __builtin_elementwise_max(mx, gv[j]);
   const int m1 = mx.x > mx.y ? mx.x : mx.y;  // int16 max: the best non-negative-sign half
-  const int m2 = mn.x < mn.y ? mn.x : mn.y;
+  int m2 = 32767;
+  if (ballot(m1 < 0)) {
+    short2_t mn = as_s2(vec_min2(v[0]));
+#pragma unroll
+    for (int j = 1; j < VPT; ++j) mn = __builtin_elementwise_min(mn, as_s2(vec_min2(v[j])));
+    m2 = mn.x < mn.y ? mn.x : mn.y;
+  }
   const u32 best_key = desc_key(static_cast<u32>(m1 >= 0 ? m1 : m2) & 0xffffu);
   TOPK_TRACE(1);
   TOPK_WTRACE(1);
@@ -803,13 +807,6 @@ segmented_topk_kernel(TopkParams p) {
     const u32 span_hi = (span << 16) | 0xffffu;
     uint4* st_vec = reinterpret_cast<uint4*>(sm.stage + wid * kStageWords);
     u32* st_pos = sm.stage + wid * kStageWords + 256;
-    // Per-lane bit mask of the passing vectors (vector ALU only), OR-reduced over the wave.
-    u32 lane_bits = 0;
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      lane_bits |= (static_cast<u32>(static_cast<int>(t_lo) - 1 - gm[j]) >> 31) << j;
-    }
-    const u32 hv = wave_or(lane_bits);
     TOPK_WTRACE(2);
     u32 nst = 0;  // staged vectors (wave-uniform)
     auto flush = [&]() {
@@ -851,37 +848,24 @@ segmented_topk_kernel(TopkParams p) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       nst = 0;
     };
-    // Stage the passing vectors: a loop over the wave's passing vector indices, reading the
-    // vector at a uniform register index.
-    constexpr int NG = (VPT + 7) / 8;  // groups of 8 vectors
-    u32x32_t vv[NG];
+    // Stage the passing vectors: one compare and ballot per vector gives the wave's passing
+    // lanes, and a wave-uniform branch skips the vectors no lane passes.
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      u32x32_t& dst = vv[j >> 3];
-      const int b = (j & 7) * 4;
-      dst[b] = v[j].x;
-      dst[b + 1] = v[j].y;
-      dst[b + 2] = v[j].z;
-      dst[b + 3] = v[j].w;
-    }
-    auto stage = [&](const u32x32_t& a, u32 bits, int jbase) {
-      while (bits) {
-        const int jj = __builtin_ctz(bits);
-        bits &= bits - 1;
-        const bool mine = (lane_bits >> (jbase + jj)) & 1u;
-        const u64 m = ballot(mine);
+      const int gmax = gv[j].x > gv[j].y ? gv[j].x : gv[j].y;
+      const bool mine = gmax >= static_cast<int>(t_lo);
+      const u64 m = ballot(mine);
+      if (m) {
         const u32 c = static_cast<u32>(__popcll(m));
         if (nst + c > 64u) flush();
         if (mine) {
           const u32 slot = nst + mbcnt(m);
-          st_vec[slot] = make_uint4(a[jj * 4], a[jj * 4 + 1], a[jj * 4 + 2], a[jj * 4 + 3]);
-          st_pos[slot] = static_cast<u32>(((jbase + jj) * BLOCK + tid) * 8);
+          st_vec[slot] = v[j];
+          st_pos[slot] = static_cast<u32>((j * BLOCK + tid) * 8);
         }
         nst += c;
       }
-    };
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) stage(vv[gi], (hv >> (8 * gi)) & 0xffu, 8 * gi);
+    }
     TOPK_WTRACE(3);
     if (nst) flush();
     TOPK_WTRACE(4);
