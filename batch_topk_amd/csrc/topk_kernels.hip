@@ -72,7 +72,10 @@ typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 // a data-dependent set of a lane's vectors compiles to one short body instead of one per vector.
 typedef unsigned u32x32_t __attribute__((ext_vector_type(32)));
 
-constexpr u32 kFillWord = 0xFFFFFFFFu;  // two negative NaNs: never a candidate, never a best
+// Word 3 of a gfx9 buffer resource (raw, untyped: data format 32 bits) and the nontemporal
+// cache policy of a buffer load.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kCachePolicyNT = 2;
 constexpr int kArea = kCandArea;        // LDS candidate entries (candidate list, merged lists)
 constexpr int kRankCap = 512;           // rank-counting path handles up to this many
 
@@ -328,6 +331,37 @@ __device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u
   if (lane < count && my_rank < kk) write_rank(p, n, seg, my_rank, mine);
 }
 
+// Ranks the M (<= 128) unique candidates of `list` and writes those of rank < kk.  One DPP
+// row (16 lanes) per candidate: lane q of the row compares it with entries q, q + 16, ... (held
+// in registers, loaded once), and a row prefix sum leaves its rank in the row's last lane,
+// which writes the output entry.  The rows take the candidates in turn.
+template <int BLOCK>
+__device__ void row_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M, int kk) {
+  constexpr int ROWS = BLOCK / 16;
+  const int row = threadIdx.x >> 4;
+  const int q = threadIdx.x & 15;
+  u64 ent[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int i = q + 16 * t;
+    ent[t] = ~0ull;
+    if (16 * t < M) ent[t] = i < M ? list[i] : ~0ull;  // uniform: no LDS read past the list
+  }
+  TOPK_WTRACE(6);
+  for (int c = row; c < M; c += ROWS) {  // uniform within each row
+    const u64 x = list[c];
+    u32 cnt = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) cnt += ent[t] < x ? 1u : 0u;
+    cnt += dpp<0x111, 0xf>(cnt);
+    cnt += dpp<0x112, 0xf>(cnt);
+    cnt += dpp<0x114, 0xf>(cnt);
+    cnt += dpp<0x118, 0xf>(cnt);
+    if (q == 15 && cnt < static_cast<u32>(kk)) write_rank(p, n, seg, static_cast<int>(cnt), x);
+  }
+  TOPK_WTRACE(7);
+}
+
 // Select the kk best of the M packed candidates in `sm.area` (M >= kk) and write them, in
 // order, to the segment's output row; ranks kk..k-1 get the pad (index -1, bits 0xFFFF).
 template <int BLOCK>
@@ -346,7 +380,7 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
   // Small sets: every wave ranks its share against the whole list held in registers and
   // writes the output entries of its candidates that rank below kk.
   if (M <= 128) {
-    wave_rank_write<BLOCK, 2>(p, n, seg, sm.area, M, kk);
+    row_rank_write<BLOCK>(p, n, seg, sm.area, M, kk);
     return;
   }
   if constexpr (NW >= 8) {
@@ -397,6 +431,15 @@ __device__ __forceinline__ bool arrive_last(u64* ticket, u64 epoch, int arrivals
       return last;
     }
   }
+}
+
+// Orders a wave's LDS writes before its lanes read each other's entries (and the reads before
+// the next overwrite): LDS requests of one wave are served in order, so this only has to keep
+// the compiler from moving them across.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ __forceinline__ void wait_vector_memory() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -600,13 +643,6 @@ __device__ void rank_range_write(const TopkParams& p, int64_t n, int seg, const 
   }
 }
 
-// Nontemporal 16-byte load at a 32-bit byte offset from a wave-uniform base (so the
-// address stays in the scalar base + 32-bit vector offset form).
-__device__ __forceinline__ uint4 load_nt(const unsigned char* base, u32 byte_off) {
-  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + byte_off));
-  return make_uint4(t.x, t.y, t.z, t.w);
-}
-
 __device__ __forceinline__ short2_t as_s2(u32 w) { return __builtin_bit_cast(short2_t, w); }
 __device__ __forceinline__ u32 as_u32(short2_t w) { return __builtin_bit_cast(u32, w); }
 
@@ -703,32 +739,40 @@ segmented_topk_kernel(TopkParams p) {
     }
   }
 
-  // ---- 1. load the chunk: all nontemporal 16-byte loads issued before any is consumed; a
-  // block with no element of the chunk re-reads the chunk's first block (always in bounds).
+  // ---- 1. load the chunk: all nontemporal 16-byte loads issued before any is consumed.
+  // Buffer loads from the chunk's base: vector j of thread tid is at byte tid * 16 (one VGPR
+  // for every j) plus j * BLOCK * 16 (a scalar offset).  The buffer ends at the first 8-block
+  // boundary at or past hi, so a vector wholly past the chunk reads as zero without touching
+  // memory; the vector holding hi is read whole, as the refinement re-read below also does.
   uint4 v[VPT];
   const unsigned char* cptr = reinterpret_cast<const unsigned char*>(p.base + cb);
-  const u32 lo_blk = static_cast<u32>(lo & ~7);
-  const u32 any_lo = static_cast<u32>(lo - 7);             // a block holds an element of [lo, hi)
-  const u32 any_span = static_cast<u32>(hi) - any_lo;      // iff pos - (lo - 7) < hi - (lo - 7)
+  {
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(cptr), static_cast<short>(0), ((hi + 7) & ~7) * 2, kBufferWord3);
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const u32 pos = static_cast<u32>((j * BLOCK + tid) * 8);
-    const bool any = pos - any_lo < any_span;
-    v[j] = load_nt(cptr, (any ? pos : lo_blk) * 2u);
+    for (int j = 0; j < VPT; ++j) {
+      const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, tid * 16, j * BLOCK * 16, kCachePolicyNT);
+      v[j] = make_uint4(t.x, t.y, t.z, t.w);
+    }
   }
   for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
   __syncthreads();  // histogram cleared (the loads stay in flight)
   TOPK_TRACE(12);
+  // Positions outside [lo, hi) become the filler.  lo > 0 only in a segment's first chunk,
+  // where it is below 8, so only vector 0 can start before lo; whether a vector index reaches
+  // past hi is workgroup-uniform, so the per-lane test runs only for those vectors.
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int pos = (j * BLOCK + tid) * 8;
-    if (pos < lo || pos + 8 > hi) {  // edge or empty block: fill outside [lo, hi)
-      u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    if ((j == 0 && lo > 0) || (j + 1) * BLOCK * 8 > hi) {
+      const int pos = (j * BLOCK + tid) * 8;
+      if (pos < lo || pos + 8 > hi) {
+        u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (pos + e < lo || pos + e >= hi) w4[e >> 1] |= 0xffffu << ((e & 1) * 16);
+        for (int e = 0; e < 8; ++e) {
+          if (pos + e < lo || pos + e >= hi) w4[e >> 1] |= 0xffffu << ((e & 1) * 16);
+        }
+        v[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
       }
-      v[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
     }
   }
 
@@ -789,10 +833,16 @@ segmented_topk_kernel(TopkParams p) {
   TOPK_WTRACE(0);
 
   // ---- 4. filter {key <= T} into the contiguous LDS candidate list, packed as
-  // (key16 << 48 | index32 << 16 | raw16).  Scheduling matters more than work here: the
-  // waves' instruction streams are latency-bound and LDS instructions are serialised per CU.
+  // (key16 << 48 | index32 << 16 | raw16).  Instruction counts matter more than latency here:
+  // the 16 waves of a CU share its scalar unit and LDS, and each SIMD issues for 4 waves.
   const bool all_mode = T == 0xffffu;  // no usable threshold: fewer than kc bests, or NaNs
-  if (!all_mode && T < 0x7fffu) {
+  // Each thread best with key <= T is an element with key <= T: when more of them exist than
+  // list entries (ties, all-equal rows) the list overflows for certain, and the refinement
+  // below takes over without filtering.  (Cooperative counts cover the whole segment.)
+  const int npass = sm.scal[9] + sm.scal[13] + sm.scal[14];
+  const bool sure_overflow = !COOP && !all_mode && npass > kArea;
+  const bool filter = !all_mode && !sure_overflow;
+  if (filter && T < 0x7fffu) {
     // T is a positive value: candidates are the b in [raw(T), 0x7C00] (positive, non-NaN).
     // A vector can hold one only if the int16 max of its halves is >= raw(T).  Each wave
     // copies its lanes' vectors that pass this test into an LDS staging list (one 16-byte
@@ -809,49 +859,47 @@ segmented_topk_kernel(TopkParams p) {
     u32* st_pos = sm.stage + wid * kStageWords + 256;
     TOPK_WTRACE(2);
     u32 nst = 0;  // staged vectors (wave-uniform)
+    // Tests the nst staged vectors one per lane and appends their hits to the list.
     auto flush = [&]() {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const bool valid = static_cast<u32>(lane) < nst;
-      const uint4 x = st_vec[lane];
-      const u32 p0 = idx_base + st_pos[lane];
-      const u32 w4[4] = {x.x, x.y, x.z, x.w};
-      bool h[8];
-      u32 cnt = 0;
+      wave_lds_sync();
+      u32 w4[4] = {0u, 0u, 0u, 0u};
+      u32 hm = 0;  // hits among the 8 halves of this lane's staged vector
+      u32 p0 = 0;
+      if (static_cast<u32>(lane) < nst) {
+        const uint4 x = st_vec[lane];
+        w4[0] = x.x; w4[1] = x.y; w4[2] = x.z; w4[3] = x.w;
+        p0 = idx_base + st_pos[lane];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const u32 d = __builtin_bit_cast(u32, __builtin_bit_cast(ushort2_t, w4[q]) - tt);
-        h[2 * q] = valid && static_cast<unsigned short>(d) <= span;
-        h[2 * q + 1] = valid && d <= span_hi;
-        cnt += static_cast<u32>(h[2 * q]) + static_cast<u32>(h[2 * q + 1]);
+        for (int q = 0; q < 4; ++q) {
+          const u32 d = __builtin_bit_cast(u32, __builtin_bit_cast(ushort2_t, w4[q]) - tt);
+          hm |= static_cast<u32>(static_cast<unsigned short>(d) <= span) << (2 * q);
+          hm |= static_cast<u32>(d <= span_hi) << (2 * q + 1);
+        }
       }
+      const u32 cnt = static_cast<u32>(__builtin_popcount(hm));
       const u32 incl = wave_inclusive_scan(cnt);
       const u32 total = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
       if (total) {
         u32 base = 0;
         if (lane == 0) base = atomicAdd(reinterpret_cast<u32*>(&sm.scal[4]), total);
         u32 o = __builtin_amdgcn_readfirstlane(base) + incl - cnt;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (h[e]) {
-            const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-            const u32 pi = p0 + static_cast<u32>(e);
-            if (o < static_cast<u32>(kArea))
-              sm.area[o] = (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b);
-            ++o;
-          }
+        while (hm) {
+          const u32 e = static_cast<u32>(__builtin_ctz(hm));
+          hm &= hm - 1u;
+          const u32 word = e < 2u ? w4[0] : (e < 4u ? w4[1] : (e < 6u ? w4[2] : w4[3]));
+          const u32 b = (word >> ((e & 1u) * 16u)) & 0xffffu;
+          const u32 pi = p0 + e;
+          if (o < static_cast<u32>(kArea))
+            sm.area[o] = (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b);
+          ++o;
         }
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      wave_lds_sync();
       nst = 0;
     };
     // Stage the passing vectors: one compare and ballot per vector gives the wave's passing
     // lanes, and a wave-uniform branch skips the vectors no lane passes.
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
+    auto stage_vector = [&](int j) {  // inlined into unrolled loops: j is a constant
       const int gmax = gv[j].x > gv[j].y ? gv[j].x : gv[j].y;
       const bool mine = gmax >= static_cast<int>(t_lo);
       const u64 m = ballot(mine);
@@ -865,11 +913,13 @@ segmented_topk_kernel(TopkParams p) {
         }
         nst += c;
       }
-    }
+    };
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) stage_vector(j);
     TOPK_WTRACE(3);
     if (nst) flush();
     TOPK_WTRACE(4);
-  } else if (!all_mode) {
+  } else if (filter) {
     // T is +-0 or negative: candidates are every non-NaN positive and the b with
     // uint16(b) <= raw(T) (raw of the zero class taken as 0x8000).  Each wave collects its hits
     // in a private LDS region (ballot/mbcnt slots), then reserves its share of the list with
@@ -899,9 +949,7 @@ segmented_topk_kernel(TopkParams p) {
     // A region that overflowed forces the exact refinement by pushing the count past kArea.
     const u32 amount = wcount > static_cast<u32>(RC) ? static_cast<u32>(kArea) + 1u : wcount;
     if (amount) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      wave_lds_sync();
       u32 base = 0;
       if (lane == 0) base = atomicAdd(reinterpret_cast<u32*>(&sm.scal[4]), amount);
       base = __builtin_amdgcn_readfirstlane(base);
@@ -916,7 +964,7 @@ segmented_topk_kernel(TopkParams p) {
   __syncthreads();
   TOPK_WTRACE(5);
 
-  int C = all_mode ? 0 : sm.scal[4];
+  int C = all_mode ? 0 : (sure_overflow ? kArea + 1 : sm.scal[4]);
   const bool overflow = C > kArea;
   // Re-reads the chunk from memory and calls fn(raw bits, chunk position) for every element
   // in [lo, hi): the refinement passes do not keep the fast path's registers live.

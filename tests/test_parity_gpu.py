@@ -138,6 +138,23 @@ def test_edge_rows(name, k):
     assert_properties(bits, vals, idx, k, [bits.shape[1]] * bits.shape[0])
 
 
+@pytest.mark.parametrize("seg_len", [4096, 32000, 128256])
+@pytest.mark.parametrize("k", [1, 50])
+def test_top_values_next_to_positive_nans(seg_len, k):
+    # Every top element shares its 16-byte vector with a positive NaN (0x7E00 / 0x7C01 /
+    # 0x7FFF), so the raw int16 maximum of every lane holding a top element is a NaN.  Those
+    # lanes must still be searched for candidates (a NaN is the worst value, never selected
+    # ahead of a real one).
+    rng = np.random.default_rng(seg_len + k)
+    bits = rng.standard_normal((4, seg_len)).astype(np.float16).view(np.uint16)
+    nans = np.array([0x7E00, 0x7C01, 0x7FFF], dtype=np.uint16)
+    for r in range(bits.shape[0]):
+        top = rng.choice(seg_len, size=60, replace=False)
+        bits[r, top] = (np.float16(40.0) + rng.integers(0, 8, size=60).astype(np.float16)).view(np.uint16)
+        bits[r, top ^ 1] = nans[rng.integers(0, 3, size=60)]
+    check_fixed(bits, k, f"top values beside positive NaNs seg_len={seg_len}")
+
+
 @pytest.mark.parametrize("seg_len,k", [(1, 1), (7, 7), (8, 3), (63, 63), (64, 50), (65, 64),
                                        (257, 256), (1000, 1000), (4096, 1024), (4097, 1)])
 def test_small_and_k_equal_len(seg_len, k):
