@@ -32,6 +32,10 @@ EXPORTED_SYMBOLS = (
     "radix_topk_batch_topk_half_workspace_size",
     "radix_topk_batch_topk_half_segmented",
     "radix_topk_batch_topk_half_segmented_workspace_size",
+    "radix_topk_batch_topk_bf16",
+    "radix_topk_batch_topk_bf16_workspace_size",
+    "radix_topk_batch_topk_bf16_segmented",
+    "radix_topk_batch_topk_bf16_segmented_workspace_size",
 )
 
 _lib = None
@@ -62,6 +66,14 @@ def load_library():
         L.radix_topk_batch_topk_half_segmented.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, sz, vp]
         L.radix_topk_batch_topk_half_segmented_workspace_size.restype = sz
         L.radix_topk_batch_topk_half_segmented_workspace_size.argtypes = [i32, i32, i32]
+        L.radix_topk_batch_topk_bf16.restype = i32
+        L.radix_topk_batch_topk_bf16.argtypes = [vp, i32, i32, i32, vp, vp, vp, sz, vp]
+        L.radix_topk_batch_topk_bf16_workspace_size.restype = sz
+        L.radix_topk_batch_topk_bf16_workspace_size.argtypes = [i32, i32, i32]
+        L.radix_topk_batch_topk_bf16_segmented.restype = i32
+        L.radix_topk_batch_topk_bf16_segmented.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, sz, vp]
+        L.radix_topk_batch_topk_bf16_segmented_workspace_size.restype = sz
+        L.radix_topk_batch_topk_bf16_segmented_workspace_size.argtypes = [i32, i32, i32]
         _lib = L
     return _lib
 
@@ -96,7 +108,46 @@ def batch_topk_half_segmented_workspace_size(seg_num: int, max_seg_len: int, k: 
         seg_num, max_seg_len, k))
 
 
+def batch_topk_bf16(d_input: int, seg_num: int, seg_len: int, k: int, d_output_values: int,
+                    d_output_indices: int, d_workspace: int, workspace_bytes: int,
+                    stream: int = 0) -> int:
+    """bfloat16 twin of batch_topk_half (same arguments and contract) -> hipError_t code."""
+    return int(load_library().radix_topk_batch_topk_bf16(
+        d_input, seg_num, seg_len, k, d_output_values, d_output_indices, d_workspace,
+        workspace_bytes, stream))
+
+
+def batch_topk_bf16_workspace_size(seg_num: int, seg_len: int, k: int) -> int:
+    return int(load_library().radix_topk_batch_topk_bf16_workspace_size(seg_num, seg_len, k))
+
+
+def batch_topk_bf16_segmented(d_input: int, d_offsets: int, seg_num: int, max_seg_len: int,
+                              k: int, d_output_values: int, d_output_indices: int,
+                              d_workspace: int, workspace_bytes: int, stream: int = 0) -> int:
+    """bfloat16 twin of batch_topk_half_segmented -> hipError_t code."""
+    return int(load_library().radix_topk_batch_topk_bf16_segmented(
+        d_input, d_offsets, seg_num, max_seg_len, k, d_output_values, d_output_indices,
+        d_workspace, workspace_bytes, stream))
+
+
+def batch_topk_bf16_segmented_workspace_size(seg_num: int, max_seg_len: int, k: int) -> int:
+    return int(load_library().radix_topk_batch_topk_bf16_segmented_workspace_size(
+        seg_num, max_seg_len, k))
+
+
 # ------------------------------------------------------------------ torch conveniences
+
+def _entry_points(dtype):
+    """(fixed, fixed workspace, segmented, segmented workspace) for a torch dtype."""
+    import torch
+
+    if dtype == torch.float16:
+        return (batch_topk_half, batch_topk_half_workspace_size, batch_topk_half_segmented,
+                batch_topk_half_segmented_workspace_size)
+    if dtype == torch.bfloat16:
+        return (batch_topk_bf16, batch_topk_bf16_workspace_size, batch_topk_bf16_segmented,
+                batch_topk_bf16_segmented_workspace_size)
+    raise ValueError(f"unsupported dtype {dtype}: float16 or bfloat16")
 
 def _stream_handle(stream) -> int:
     import torch
@@ -106,53 +157,55 @@ def _stream_handle(stream) -> int:
 
 
 def topk(x, k: int, workspace=None, stream=None):
-    """Top-k of every row of a contiguous fp16 CUDA tensor [seg_num, seg_len].
+    """Top-k of every row of a contiguous float16 or bfloat16 CUDA tensor [seg_num, seg_len].
 
-    Returns (values fp16 [seg_num, k], indices int32 [seg_num, k]).  ``workspace`` may be a
-    uint8 CUDA tensor of at least ``batch_topk_half_workspace_size`` bytes.
+    Returns (values [seg_num, k] of x's dtype, indices int32 [seg_num, k]).  ``workspace``
+    may be a uint8 CUDA tensor of at least the workspace size of the shape.
     """
     import torch
 
-    if x.dtype != torch.float16 or x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
-        raise ValueError("topk expects a contiguous 2-D float16 CUDA tensor")
+    if x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
+        raise ValueError("topk expects a contiguous 2-D float16 or bfloat16 CUDA tensor")
+    fixed, fixed_ws, _, _ = _entry_points(x.dtype)
     seg_num, seg_len = x.shape
-    ws_bytes = batch_topk_half_workspace_size(seg_num, seg_len, k)
+    ws_bytes = fixed_ws(seg_num, seg_len, k)
     if ws_bytes == 0:
-        raise TopkError(HIP_ERROR_INVALID_VALUE, "batch_topk_half_workspace_size")
+        raise TopkError(HIP_ERROR_INVALID_VALUE, f"{fixed.__name__}_workspace_size")
     if workspace is None:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
-    vals = torch.empty((seg_num, k), dtype=torch.float16, device=x.device)
+    vals = torch.empty((seg_num, k), dtype=x.dtype, device=x.device)
     idx = torch.empty((seg_num, k), dtype=torch.int32, device=x.device)
-    rc = batch_topk_half(x.data_ptr(), seg_num, seg_len, k, vals.data_ptr(), idx.data_ptr(),
-                         workspace.data_ptr(), workspace.numel(), _stream_handle(stream))
+    rc = fixed(x.data_ptr(), seg_num, seg_len, k, vals.data_ptr(), idx.data_ptr(),
+               workspace.data_ptr(), workspace.numel(), _stream_handle(stream))
     if rc != HIP_SUCCESS:
-        raise TopkError(rc, "batch_topk_half")
+        raise TopkError(rc, fixed.__name__)
     return vals, idx
 
 
 def segmented_topk(x, offsets, k: int, max_seg_len: int, workspace=None, stream=None):
-    """Top-k of every segment x[offsets[s]:offsets[s+1]] of a 1-D fp16 CUDA tensor.
+    """Top-k of every segment x[offsets[s]:offsets[s+1]] of a 1-D float16 or bfloat16 CUDA
+    tensor.
 
     ``offsets`` is an int32 CUDA tensor of seg_num + 1 entries.  Ranks beyond a segment's
     length hold index -1 and value bits 0xFFFF.
     """
     import torch
 
-    if x.dtype != torch.float16 or not x.is_cuda or not x.is_contiguous():
-        raise ValueError("segmented_topk expects a contiguous float16 CUDA tensor")
+    if not x.is_cuda or not x.is_contiguous():
+        raise ValueError("segmented_topk expects a contiguous float16 or bfloat16 CUDA tensor")
     if offsets.dtype != torch.int32 or not offsets.is_cuda or offsets.dim() != 1:
         raise ValueError("offsets must be a 1-D int32 CUDA tensor")
+    _, _, seg, seg_ws = _entry_points(x.dtype)
     seg_num = offsets.numel() - 1
-    ws_bytes = batch_topk_half_segmented_workspace_size(seg_num, max_seg_len, k)
+    ws_bytes = seg_ws(seg_num, max_seg_len, k)
     if ws_bytes == 0:
-        raise TopkError(HIP_ERROR_INVALID_VALUE, "batch_topk_half_segmented_workspace_size")
+        raise TopkError(HIP_ERROR_INVALID_VALUE, f"{seg.__name__}_workspace_size")
     if workspace is None:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
-    vals = torch.empty((seg_num, k), dtype=torch.float16, device=x.device)
+    vals = torch.empty((seg_num, k), dtype=x.dtype, device=x.device)
     idx = torch.empty((seg_num, k), dtype=torch.int32, device=x.device)
-    rc = batch_topk_half_segmented(x.data_ptr(), offsets.data_ptr(), seg_num, max_seg_len, k,
-                                   vals.data_ptr(), idx.data_ptr(), workspace.data_ptr(),
-                                   workspace.numel(), _stream_handle(stream))
+    rc = seg(x.data_ptr(), offsets.data_ptr(), seg_num, max_seg_len, k, vals.data_ptr(),
+             idx.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream_handle(stream))
     if rc != HIP_SUCCESS:
-        raise TopkError(rc, "batch_topk_half_segmented")
+        raise TopkError(rc, seg.__name__)
     return vals, idx

@@ -135,9 +135,9 @@ uint64_t next_epoch() {
   }
 }
 
-int run(const Plan& plan, const uint16_t* d_input, const int32_t* d_offsets, int seg_num,
-        int64_t seg_len, int64_t max_len, int k, uint16_t* d_values, int32_t* d_indices, void* d_workspace,
-        size_t workspace_bytes, void* stream) {
+int run(const Plan& plan, uint32_t inf_bits, const uint16_t* d_input, const int32_t* d_offsets,
+        int seg_num, int64_t seg_len, int64_t max_len, int k, uint16_t* d_values, int32_t* d_indices,
+        void* d_workspace, size_t workspace_bytes, void* stream) {
   if (!plan.ok || workspace_bytes < plan.ws_bytes) return kInvalid;
   const uintptr_t in_addr = reinterpret_cast<uintptr_t>(d_input);
   if ((in_addr & 1u) || (reinterpret_cast<uintptr_t>(d_values) & 1u) ||
@@ -172,37 +172,63 @@ int run(const Plan& plan, const uint16_t* d_input, const int32_t* d_offsets, int
     p.lists = reinterpret_cast<unsigned long long*>(ws + off);
   }
   p.epoch = next_epoch();
+  p.inf_bits = inf_bits;
   return launch_segmented_topk(plan, p, stream);
+}
+
+size_t fixed_workspace_size(int seg_num, int seg_len, int k) {
+  if (seg_num <= 0 || seg_len <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K || k > seg_len) return 0;
+  const Plan plan = make_plan(seg_num, seg_len, k);
+  return plan.ok ? plan.ws_bytes : 0;
+}
+
+int fixed_topk(uint32_t inf_bits, const uint16_t* d_input, int seg_num, int seg_len, int k,
+               uint16_t* d_output_values, int32_t* d_output_indices, void* d_workspace,
+               size_t workspace_bytes, void* stream) {
+  if (seg_num <= 0 || seg_len <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K || k > seg_len) return kInvalid;
+  if (!d_input || !d_output_values || !d_output_indices || !d_workspace) return kInvalid;
+  const Plan plan = make_plan(seg_num, seg_len, k);
+  return run(plan, inf_bits, d_input, nullptr, seg_num, seg_len, seg_len, k, d_output_values,
+             d_output_indices, d_workspace, workspace_bytes, stream);
+}
+
+size_t segmented_workspace_size(int seg_num, int max_seg_len, int k) {
+  if (seg_num <= 0 || max_seg_len < 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return 0;
+  const Plan plan = make_plan(seg_num, max_seg_len, k);
+  return plan.ok ? plan.ws_bytes : 0;
+}
+
+int segmented_topk(uint32_t inf_bits, const uint16_t* d_input, const int32_t* d_offsets, int seg_num,
+                   int max_seg_len, int k, uint16_t* d_output_values, int32_t* d_output_indices,
+                   void* d_workspace, size_t workspace_bytes, void* stream) {
+  if (seg_num <= 0 || max_seg_len < 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return kInvalid;
+  if (!d_input || !d_offsets || !d_output_values || !d_output_indices || !d_workspace) return kInvalid;
+  const Plan plan = make_plan(seg_num, max_seg_len, k);
+  return run(plan, inf_bits, d_input, d_offsets, seg_num, 0, max_seg_len, k, d_output_values,
+             d_output_indices, d_workspace, workspace_bytes, stream);
 }
 
 }  // namespace
 }  // namespace radix_topk_amd
 
-using radix_topk_amd::kInvalid;
-using radix_topk_amd::make_plan;
+using radix_topk_amd::kInfBitsBF16;
+using radix_topk_amd::kInfBitsF16;
 
 extern "C" {
 
 size_t radix_topk_batch_topk_half_workspace_size(int seg_num, int seg_len, int k) {
-  if (seg_num <= 0 || seg_len <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K || k > seg_len) return 0;
-  const radix_topk_amd::Plan plan = make_plan(seg_num, seg_len, k);
-  return plan.ok ? plan.ws_bytes : 0;
+  return radix_topk_amd::fixed_workspace_size(seg_num, seg_len, k);
 }
 
 int radix_topk_batch_topk_half(const uint16_t* d_input, int seg_num, int seg_len, int k,
                                uint16_t* d_output_values, int32_t* d_output_indices,
                                void* d_workspace, size_t workspace_bytes, void* stream) {
-  if (seg_num <= 0 || seg_len <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K || k > seg_len) return kInvalid;
-  if (!d_input || !d_output_values || !d_output_indices || !d_workspace) return kInvalid;
-  const radix_topk_amd::Plan plan = make_plan(seg_num, seg_len, k);
-  return radix_topk_amd::run(plan, d_input, nullptr, seg_num, seg_len, seg_len, k, d_output_values,
-                             d_output_indices, d_workspace, workspace_bytes, stream);
+  return radix_topk_amd::fixed_topk(kInfBitsF16, d_input, seg_num, seg_len, k, d_output_values,
+                                    d_output_indices, d_workspace, workspace_bytes, stream);
 }
 
 size_t radix_topk_batch_topk_half_segmented_workspace_size(int seg_num, int max_seg_len, int k) {
-  if (seg_num <= 0 || max_seg_len < 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return 0;
-  const radix_topk_amd::Plan plan = make_plan(seg_num, max_seg_len, k);
-  return plan.ok ? plan.ws_bytes : 0;
+  return radix_topk_amd::segmented_workspace_size(seg_num, max_seg_len, k);
 }
 
 int radix_topk_batch_topk_half_segmented(const uint16_t* d_input, const int32_t* d_offsets,
@@ -210,11 +236,34 @@ int radix_topk_batch_topk_half_segmented(const uint16_t* d_input, const int32_t*
                                          uint16_t* d_output_values, int32_t* d_output_indices,
                                          void* d_workspace, size_t workspace_bytes,
                                          void* stream) {
-  if (seg_num <= 0 || max_seg_len < 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return kInvalid;
-  if (!d_input || !d_offsets || !d_output_values || !d_output_indices || !d_workspace) return kInvalid;
-  const radix_topk_amd::Plan plan = make_plan(seg_num, max_seg_len, k);
-  return radix_topk_amd::run(plan, d_input, d_offsets, seg_num, 0, max_seg_len, k, d_output_values,
-                             d_output_indices, d_workspace, workspace_bytes, stream);
+  return radix_topk_amd::segmented_topk(kInfBitsF16, d_input, d_offsets, seg_num, max_seg_len, k,
+                                        d_output_values, d_output_indices, d_workspace,
+                                        workspace_bytes, stream);
+}
+
+size_t radix_topk_batch_topk_bf16_workspace_size(int seg_num, int seg_len, int k) {
+  return radix_topk_amd::fixed_workspace_size(seg_num, seg_len, k);
+}
+
+int radix_topk_batch_topk_bf16(const uint16_t* d_input, int seg_num, int seg_len, int k,
+                               uint16_t* d_output_values, int32_t* d_output_indices,
+                               void* d_workspace, size_t workspace_bytes, void* stream) {
+  return radix_topk_amd::fixed_topk(kInfBitsBF16, d_input, seg_num, seg_len, k, d_output_values,
+                                    d_output_indices, d_workspace, workspace_bytes, stream);
+}
+
+size_t radix_topk_batch_topk_bf16_segmented_workspace_size(int seg_num, int max_seg_len, int k) {
+  return radix_topk_amd::segmented_workspace_size(seg_num, max_seg_len, k);
+}
+
+int radix_topk_batch_topk_bf16_segmented(const uint16_t* d_input, const int32_t* d_offsets,
+                                         int seg_num, int max_seg_len, int k,
+                                         uint16_t* d_output_values, int32_t* d_output_indices,
+                                         void* d_workspace, size_t workspace_bytes,
+                                         void* stream) {
+  return radix_topk_amd::segmented_topk(kInfBitsBF16, d_input, d_offsets, seg_num, max_seg_len, k,
+                                        d_output_values, d_output_indices, d_workspace,
+                                        workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -57,6 +57,10 @@ constexpr GroupLayout group_layout(int W) {
 // of an MI355X).
 constexpr int kMaxCoopGroups = 256;
 
+// +inf bit patterns of the two 16-bit element formats; a magnitude above it is a NaN.
+constexpr uint32_t kInfBitsF16 = 0x7C00u;
+constexpr uint32_t kInfBitsBF16 = 0x7F80u;
+
 // Kernel parameter block of the fused segmented top-k kernel.  Every segment s covers the
 // element range [s0, s1) of `base` (a 16-byte aligned pointer); s0/s1 come from the int32
 // offsets when given, else from s * seg_len.  `elem0` is the element offset of the caller's
@@ -81,6 +85,7 @@ struct TopkParams {
   int32_t* list_counts;         // [seg_num * W]
   unsigned long long* lists;    // [seg_num * W * cap_list] packed (key16 << 32 | index)
   unsigned long long epoch;     // 48-bit token unique to this call
+  uint32_t inf_bits;            // +inf pattern of the 16-bit element format (0x7C00 fp16, 0x7F80 bf16)
   unsigned char* groups;        // cooperative path: [seg_num] blocks of group_layout(W).bytes
 };
 

@@ -81,19 +81,22 @@ constexpr int kRankCap = 512;           // rank-counting path handles up to this
 
 // ------------------------------------------------------------------------------ codec
 
-// Descending order-preserving key of raw fp16 bits (reference include/type_codec.cuh:13-38):
-// NaN -> 0xFFFF, +-0 -> 0x7FFF, negative -> bits, positive -> bits ^ 0x7FFF.
-__device__ __forceinline__ u32 desc_key(u32 b) {
+// Descending order-preserving key of raw 16-bit float bits (reference
+// include/type_codec.cuh:13-38 for fp16): NaN -> 0xFFFF, +-0 -> 0x7FFF, negative -> bits,
+// positive -> bits ^ 0x7FFF.  fp16 and bf16 are both sign-magnitude with an all-ones exponent
+// for inf and NaN; `inf` is the format's +inf pattern (0x7C00 fp16, 0x7F80 bf16) and a
+// magnitude above it is a NaN.
+__device__ __forceinline__ u32 desc_key(u32 b, u32 inf) {
   const u32 mag = b & 0x7fffu;
   u32 key = (b & 0x8000u) ? b : (b ^ 0x7fffu);
   key = (mag == 0u) ? 0x7fffu : key;
-  key = (mag > 0x7c00u) ? 0xffffu : key;
+  key = (mag > inf) ? 0xffffu : key;
   return key;
 }
 
 // Candidate packing: ascending u64 order == ascending (key, index); raw bits carried along.
-__device__ __forceinline__ u64 pack_candidate(u32 raw, u32 index) {
-  return (static_cast<u64>(desc_key(raw)) << 48) | (static_cast<u64>(index) << 16) | raw;
+__device__ __forceinline__ u64 pack_candidate(u32 raw, u32 index, u32 inf) {
+  return (static_cast<u64>(desc_key(raw, inf)) << 48) | (static_cast<u64>(index) << 16) | raw;
 }
 __device__ __forceinline__ u32 cand_index(u64 P) { return static_cast<u32>(P >> 16); }
 __device__ __forceinline__ u32 cand_raw(u64 P) { return static_cast<u32>(P) & 0xffffu; }
@@ -680,6 +683,7 @@ segmented_topk_kernel(TopkParams p) {
   const int w = W == 1 ? 0 : static_cast<int>(blockIdx.x) / p.seg_num;
   const int seg = W == 1 ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) - w * p.seg_num;
   const int k = p.k;
+  const u32 inf = p.inf_bits;  // +inf bit pattern of the element format
 
   int64_t s0, s1;
   if (p.offsets) {
@@ -794,7 +798,7 @@ segmented_topk_kernel(TopkParams p) {
     for (int j = 1; j < VPT; ++j) mn = __builtin_elementwise_min(mn, as_s2(vec_min2(v[j])));
     m2 = mn.x < mn.y ? mn.x : mn.y;
   }
-  const u32 best_key = desc_key(static_cast<u32>(m1 >= 0 ? m1 : m2) & 0xffffu);
+  const u32 best_key = desc_key(static_cast<u32>(m1 >= 0 ? m1 : m2) & 0xffffu, inf);
   TOPK_TRACE(1);
   TOPK_WTRACE(1);
 
@@ -843,17 +847,17 @@ segmented_topk_kernel(TopkParams p) {
   const bool sure_overflow = !COOP && !all_mode && npass > kArea;
   const bool filter = !all_mode && !sure_overflow;
   if (filter && T < 0x7fffu) {
-    // T is a positive value: candidates are the b in [raw(T), 0x7C00] (positive, non-NaN).
+    // T is a positive value: candidates are the b in [raw(T), inf] (positive, non-NaN).
     // A vector can hold one only if the int16 max of its halves is >= raw(T).  Each wave
     // copies its lanes' vectors that pass this test into an LDS staging list (one 16-byte
     // write per such vector), then tests the staged vectors one per lane: one packed
     // subtract d = b - raw(T) per word and two unsigned compares give the exact hits
-    // (d <= 0x7C00 - raw(T) holds exactly for raw(T) <= b <= 0x7C00).  A wave prefix sum
+    // (d <= inf - raw(T) holds exactly for raw(T) <= b <= inf).  A wave prefix sum
     // gives every hit its offset, and one LDS atomic per 64 staged vectors reserves the
     // wave's slots in the list.
     const u32 t_lo = T ^ 0x7fffu;
     const ushort2_t tt = {static_cast<unsigned short>(t_lo), static_cast<unsigned short>(t_lo)};
-    const u32 span = 0x7c00u - t_lo;
+    const u32 span = inf - t_lo;
     const u32 span_hi = (span << 16) | 0xffffu;
     uint4* st_vec = reinterpret_cast<uint4*>(sm.stage + wid * kStageWords);
     u32* st_pos = sm.stage + wid * kStageWords + 256;
@@ -934,13 +938,13 @@ segmented_topk_kernel(TopkParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        const bool h = b <= traw && (b & 0x7fffu) <= 0x7c00u;
+        const bool h = b <= traw && (b & 0x7fffu) <= inf;
         const u64 m = ballot(h);
         if (m) {
           if (h) {
             const u32 slot = wcount + mbcnt(m);
             if (slot < static_cast<u32>(RC))
-              region[slot] = pack_candidate(b, idx_base + static_cast<u32>((j * BLOCK + tid) * 8 + e));
+              region[slot] = pack_candidate(b, idx_base + static_cast<u32>((j * BLOCK + tid) * 8 + e), inf);
           }
           wcount += static_cast<u32>(__popcll(m));
         }
@@ -1013,7 +1017,7 @@ segmented_topk_kernel(TopkParams p) {
         for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
         __syncthreads();
         for_each_element([&](u32 b, int pos) {
-          const u32 key = desc_key(b);
+          const u32 key = desc_key(b, inf);
           const u64 Q = (static_cast<u64>(key) << 32) | (idx_base + static_cast<u32>(pos));
           if (key <= T && (Q & pmask) == prefix) atomicAdd(&sm.hist[(Q >> shift) & 255u], 1u);
         });
@@ -1034,12 +1038,12 @@ segmented_topk_kernel(TopkParams p) {
       if (tid == 0) sm.scal[4] = 0;
       __syncthreads();
       for_each_element([&](u32 b, int pos) {
-        const u32 key = desc_key(b);
+        const u32 key = desc_key(b, inf);
         const u32 idx = idx_base + static_cast<u32>(pos);
         const u64 Q = (static_cast<u64>(key) << 32) | idx;
         if (key <= T && Q <= bound) {
           const int slot = atomicAdd(&sm.scal[4], 1);
-          if (slot < kArea) sm.area[slot] = pack_candidate(b, idx);
+          if (slot < kArea) sm.area[slot] = pack_candidate(b, idx, inf);
         }
       });
       __syncthreads();
@@ -1075,7 +1079,7 @@ segmented_topk_kernel(TopkParams p) {
       for (int e = 0; e < 8; ++e) {
         const int pos = (j * BLOCK + tid) * 8 + e;
         const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        if (pos >= lo && pos < hi) sm.area[pos - lo] = pack_candidate(b, idx_base + static_cast<u32>(pos));
+        if (pos >= lo && pos < hi) sm.area[pos - lo] = pack_candidate(b, idx_base + static_cast<u32>(pos), inf);
       }
     }
     C = nc;
@@ -1091,7 +1095,7 @@ segmented_topk_kernel(TopkParams p) {
       for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
       __syncthreads();
       for_each_element([&](u32 b, int pos) {
-        const u32 key = desc_key(b);
+        const u32 key = desc_key(b, inf);
         const u64 P = (static_cast<u64>(key) << 17) | static_cast<u32>(pos);
         if (key <= T && (P & pmask) == prefix) atomicAdd(&sm.hist[(P >> shift) & 255u], 1u);
       });
@@ -1111,11 +1115,11 @@ segmented_topk_kernel(TopkParams p) {
     if (tid == 0) sm.scal[4] = 0;
     __syncthreads();
     for_each_element([&](u32 b, int pos) {
-      const u32 key = desc_key(b);
+      const u32 key = desc_key(b, inf);
       const u64 P = (static_cast<u64>(key) << 17) | static_cast<u32>(pos);
       if (key <= T && P <= bound) {
         const int slot = atomicAdd(&sm.scal[4], 1);
-        if (slot < kArea) sm.area[slot] = pack_candidate(b, idx_base + static_cast<u32>(pos));
+        if (slot < kArea) sm.area[slot] = pack_candidate(b, idx_base + static_cast<u32>(pos), inf);
       }
     });
     __syncthreads();

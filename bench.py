@@ -17,9 +17,10 @@ Prints ONE JSON line:
 
 Other workloads (--workload uniform_small | ties_special | varlen | huge_segment, and
 ref_matrix --seg-num N for the reference's own benchmark matrix) print the same line for
-that configuration.
+that configuration.  --dtype bf16 runs the bfloat16 entry points on the same workload
+rounded to bfloat16 (no CPU baseline: that is the reference's fp16 verifier).
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--k K]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--k K] [--dtype f16|bf16]
 """
 
 from __future__ import annotations
@@ -119,6 +120,7 @@ def main() -> int:
     ap.add_argument("--rotate-mb", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--dtype", choices=("f16", "bf16"), default="f16")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the engine has no "
@@ -133,14 +135,24 @@ def main() -> int:
     dev = torch.device("cuda:0")
     bits, offsets, cfg = make_input(args.workload, args.seg_num)
     k = args.k
+    if args.dtype == "bf16":
+        # the same workload rounded to bfloat16 (round to nearest even)
+        bits = torch.from_numpy(bits.view(np.float16).astype(np.float32)).bfloat16() \
+            .view(torch.int16).numpy().view(np.uint16)
+        cfg["workload"] += ", rounded to bfloat16"
+        fixed, fixed_ws = bt.batch_topk_bf16, bt.batch_topk_bf16_workspace_size
+        seg, seg_ws = bt.batch_topk_bf16_segmented, bt.batch_topk_bf16_segmented_workspace_size
+    else:
+        fixed, fixed_ws = bt.batch_topk_half, bt.batch_topk_half_workspace_size
+        seg, seg_ws = bt.batch_topk_half_segmented, bt.batch_topk_half_segmented_workspace_size
     if offsets is None:
         seg_num, seg_len = bits.shape
         n_elements = seg_num * seg_len
-        ws_bytes = bt.batch_topk_half_workspace_size(seg_num, seg_len, k)
+        ws_bytes = fixed_ws(seg_num, seg_len, k)
     else:
         seg_num, seg_len = offsets.size - 1, int(np.max(np.diff(offsets)))
         n_elements = int(offsets[-1])
-        ws_bytes = bt.batch_topk_half_segmented_workspace_size(seg_num, cfg["max_seg_len"], k)
+        ws_bytes = seg_ws(seg_num, cfg["max_seg_len"], k)
         d_off = torch.from_numpy(offsets.astype(np.int32)).to(dev)
     if ws_bytes == 0:
         raise SystemExit(f"shape not supported: {cfg} k={k}")
@@ -157,12 +169,11 @@ def main() -> int:
 
     def call(i: int) -> None:
         if offsets is None:
-            rc = bt.batch_topk_half(inputs[i % copies].data_ptr(), seg_num, seg_len, k, vals.data_ptr(),
-                                    idx.data_ptr(), ws.data_ptr(), ws_bytes, sh)
+            rc = fixed(inputs[i % copies].data_ptr(), seg_num, seg_len, k, vals.data_ptr(),
+                       idx.data_ptr(), ws.data_ptr(), ws_bytes, sh)
         else:
-            rc = bt.batch_topk_half_segmented(inputs[i % copies].data_ptr(), d_off.data_ptr(), seg_num,
-                                              cfg["max_seg_len"], k, vals.data_ptr(), idx.data_ptr(),
-                                              ws.data_ptr(), ws_bytes, sh)
+            rc = seg(inputs[i % copies].data_ptr(), d_off.data_ptr(), seg_num, cfg["max_seg_len"], k,
+                     vals.data_ptr(), idx.data_ptr(), ws.data_ptr(), ws_bytes, sh)
         if rc != 0:
             raise RuntimeError(f"top-k call returned {rc}")
 
@@ -176,9 +187,10 @@ def main() -> int:
     call(0)
     torch.cuda.synchronize()
     if offsets is None:
-        ev, ei = O.batch_topk_half(bits[:8], k, seg_len=seg_len)
+        ev, ei = O.batch_topk_half(bits[:8], k, seg_len=seg_len, fmt=args.dtype)
     else:
-        ev, ei = O.batch_topk_half(bits[:int(offsets[8])], k, offsets=offsets[:9].astype(np.int64))
+        ev, ei = O.batch_topk_half(bits[:int(offsets[8])], k, offsets=offsets[:9].astype(np.int64),
+                                   fmt=args.dtype)
     gi = idx.cpu().numpy()[:8]
     gv = vals.cpu().numpy().view(np.uint16)[:8]
     parity_ok = bool(np.array_equal(gi, ei) and np.array_equal(gv, ev))
@@ -220,8 +232,9 @@ def main() -> int:
     step_us = ms_per_step * 1e3
     achieved = alg_bytes / (step_us * 1e-6)
     value = seg_num * steps / (total_ms * 1e-3)
-    metric = METRIC if (args.workload == "llm_logits" and k == 50) else \
-        f"segments/s and achieved HBM GB/s, fp16 top-{k} over {cfg['workload'].split(':')[0]}"
+    dname = "fp16" if args.dtype == "f16" else "bf16"
+    metric = METRIC if (args.workload == "llm_logits" and k == 50 and args.dtype == "f16") else \
+        f"segments/s and achieved HBM GB/s, {dname} top-{k} over {cfg['workload'].split(':')[0]}"
     result = {
         "metric": metric,
         "value": value,
@@ -233,7 +246,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u16",
+        "dtype": "u16" if args.dtype == "f16" else "u16 (bf16 keys)",
         "data": "synthetic",
         "config": dict(cfg, k=k, input_copies=copies, parallelism="single GPU"),
         "roofline": {
@@ -242,7 +255,7 @@ def main() -> int:
             "peak": HBM_PEAK_BPS / 1e9,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_BPS,
-            "traffic": load_traffic(args.workload, k),
+            "traffic": load_traffic(args.workload if args.dtype == "f16" else f"{args.workload}:bf16", k),
         },
         "elements_per_s": n_elements * steps / (total_ms * 1e-3),
         "hbm_gbps_whole_job": alg_bytes * steps / (total_ms * 1e-3) / 1e9,
@@ -258,7 +271,7 @@ def main() -> int:
         target = REF_MATRIX_TARGET_US.get((seg_num, seg_len, k))
         result["reference_target_us_rtx4080"] = target
         result["target_over_measured"] = None if target is None else target / (ms_per_step * 1e3)
-    if not args.no_cpu_baseline and offsets is None:
+    if not args.no_cpu_baseline and offsets is None and args.dtype == "f16":
         log("timing the CPU baseline (reference host verifier)...")
         t0 = time.time()
         result["cpu_baseline"] = cpu_baseline(bits, k, args.cpu_threads)

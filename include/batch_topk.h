@@ -84,6 +84,26 @@ int radix_topk_batch_topk_half_segmented(const uint16_t* d_input, const int32_t*
  */
 size_t radix_topk_batch_topk_half_segmented_workspace_size(int seg_num, int max_seg_len, int k);
 
+/*
+ * bfloat16 twins of the four entry points above: the same arguments, contract, workspace
+ * sizes and error behaviour, for segments of bfloat16 bit patterns.  The order is the same
+ * total order (larger value first, equal values by ascending index, every NaN below -inf,
+ * +0 equal to -0), with bfloat16's own inf/NaN boundary (exponent all ones).  No
+ * counterpart in the reference, whose codec covers fp16 only (reference
+ * include/type_codec.cuh:9-38); bfloat16 widens exactly to float, so the reference's
+ * verifier order (include/batch_topk_types.cuh:70-82) applies to it unchanged.
+ */
+int radix_topk_batch_topk_bf16(const uint16_t* d_input, int seg_num, int seg_len, int k,
+                               uint16_t* d_output_values, int32_t* d_output_indices,
+                               void* d_workspace, size_t workspace_bytes, void* stream);
+size_t radix_topk_batch_topk_bf16_workspace_size(int seg_num, int seg_len, int k);
+int radix_topk_batch_topk_bf16_segmented(const uint16_t* d_input, const int32_t* d_offsets,
+                                         int seg_num, int max_seg_len, int k,
+                                         uint16_t* d_output_values, int32_t* d_output_indices,
+                                         void* d_workspace, size_t workspace_bytes,
+                                         void* stream);
+size_t radix_topk_batch_topk_bf16_segmented_workspace_size(int seg_num, int max_seg_len, int k);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

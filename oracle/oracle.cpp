@@ -24,6 +24,10 @@
 // the header comment of oracle/oracle.py and exercised by tests/test_oracle.py.
 //
 // Extensions beyond the reference (documented decisions, not restatements):
+//   * bfloat16 segments (oracle_batch_topk_bf16): the same verifier on the exact
+//     bfloat16 -> float widening (the 16 bits become the float's high half), so the
+//     reference's comparator applies unchanged; its key (oracle_encode_bf16_desc) is the
+//     reference codec's pattern with bfloat16's inf/NaN boundary (0x7F80);
 //   * variable-length segments given by an int64 offset array;
 //   * ranks >= min(k, len) of a short segment are padded with index -1 and value bits 0xFFFF.
 
@@ -62,6 +66,14 @@ float half_bits_to_float(uint16_t h) {
   } else {
     out = sign | ((exp + 127 - 15) << 23) | (man << 13);
   }
+  float f;
+  std::memcpy(&f, &out, sizeof(f));
+  return f;
+}
+
+// Exact bfloat16 -> binary32 widening: bfloat16 is the high half of a binary32.
+float bf16_bits_to_float(uint16_t h) {
+  const uint32_t out = static_cast<uint32_t>(h) << 16;
   float f;
   std::memcpy(&f, &out, sizeof(f));
   return f;
@@ -116,6 +128,15 @@ uint16_t encode_half_asc(uint16_t raw) {
 uint16_t encode_half_desc(uint16_t raw) {
   // include/type_codec.cuh:36-38
   return static_cast<uint16_t>(~encode_half_asc(raw));
+}
+
+// The codec's pattern (include/type_codec.cuh:13-38) with bfloat16's boundary: NaN (exponent
+// all ones, mantissa nonzero; any sign or payload) -> 0xffff, +-0 -> 0x7fff, negative -> bits,
+// positive -> bits ^ 0x7fff.
+uint16_t encode_bf16_desc(uint16_t raw) {
+  if ((raw & 0x7f80u) == 0x7f80u && (raw & 0x007fu) != 0) return 0xffffu;
+  if ((raw & 0x7fffu) == 0) return 0x7fffu;
+  return (raw & 0x8000u) ? raw : static_cast<uint16_t>(raw ^ 0x7fffu);
 }
 
 // include/batch_topk_types.cuh:50-92, operating on the float vector the reference builds.
@@ -202,14 +223,17 @@ SegmentState load_state(const int32_t* in) {
   return s;
 }
 
+using ToFloat = float (*)(uint16_t);
+
 void segment_topk_raw(const uint16_t* seg, int64_t len, int k, uint16_t* out_vals,
-                      int32_t* out_idx, std::vector<float>& scratch_f, std::vector<int>& scratch_i) {
-  // One segment of the verifier loop: half -> float (exact), cpu_reference_topk, value
-  // re-read raw from the input.  Ranks beyond min(k, len) get the pad (index -1, 0xFFFF).
+                      int32_t* out_idx, std::vector<float>& scratch_f, std::vector<int>& scratch_i,
+                      ToFloat to_float) {
+  // One segment of the verifier loop: 16-bit float -> float (exact), cpu_reference_topk,
+  // value re-read raw from the input.  Ranks beyond min(k, len) get the pad (index -1, 0xFFFF).
   int got = 0;
   if (len > 0) {
     scratch_f.resize(static_cast<size_t>(len));
-    for (int64_t i = 0; i < len; ++i) scratch_f[static_cast<size_t>(i)] = half_bits_to_float(seg[i]);
+    for (int64_t i = 0; i < len; ++i) scratch_f[static_cast<size_t>(i)] = to_float(seg[i]);
     scratch_i.resize(static_cast<size_t>(std::min<int64_t>(k, len)));
     got = cpu_reference_topk(scratch_f.data(), static_cast<int>(len), static_cast<int>(len), k,
                              nullptr, scratch_i.data());
@@ -246,6 +270,11 @@ uint16_t oracle_encode_half_asc(uint16_t bits) { return encode_half_asc(bits); }
 uint16_t oracle_encode_half_desc(uint16_t bits) { return encode_half_desc(bits); }
 float oracle_half_to_float(uint16_t bits) { return half_bits_to_float(bits); }
 uint16_t oracle_float_to_half(float f) { return float_to_half_rne(f); }
+uint16_t oracle_encode_bf16_desc(uint16_t bits) { return encode_bf16_desc(bits); }
+
+void oracle_bf16_to_float_array(const uint16_t* in, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = bf16_bits_to_float(in[i]);
+}
 
 void oracle_half_to_float_array(const uint16_t* in, int64_t n, float* out) {
   for (int64_t i = 0; i < n; ++i) out[i] = half_bits_to_float(in[i]);
@@ -377,9 +406,9 @@ void oracle_histogram_pass(const uint16_t* input, int n, int shift, uint16_t pre
 // float widening of the fp16 input; values are written as the raw input bits at the
 // selected index.  offsets == nullptr selects fixed-length segments of seg_len.
 // threads <= 1 runs serially, exactly like the reference harness loop.
-int oracle_batch_topk_half(const uint16_t* input, const int64_t* offsets, int seg_num,
-                           int64_t seg_len, int k, uint16_t* out_vals, int32_t* out_idx,
-                           int threads) {
+static int batch_topk_16(const uint16_t* input, const int64_t* offsets, int seg_num,
+                         int64_t seg_len, int k, uint16_t* out_vals, int32_t* out_idx,
+                         int threads, ToFloat to_float) {
   if (seg_num <= 0 || k <= 0) return 1;
   auto run = [&](int s_begin, int s_end) {
     std::vector<float> f;
@@ -388,7 +417,7 @@ int oracle_batch_topk_half(const uint16_t* input, const int64_t* offsets, int se
       int64_t b, e;
       segment_bounds(offsets, seg_len, s, &b, &e);
       segment_topk_raw(input + b, e - b, k, out_vals + static_cast<int64_t>(s) * k,
-                       out_idx + static_cast<int64_t>(s) * k, f, idx);
+                       out_idx + static_cast<int64_t>(s) * k, f, idx, to_float);
     }
   };
   if (threads <= 1 || seg_num == 1) {
@@ -404,6 +433,21 @@ int oracle_batch_topk_half(const uint16_t* input, const int64_t* offsets, int se
   }
   for (auto& th : pool) th.join();
   return 0;
+}
+
+int oracle_batch_topk_half(const uint16_t* input, const int64_t* offsets, int seg_num,
+                           int64_t seg_len, int k, uint16_t* out_vals, int32_t* out_idx,
+                           int threads) {
+  return batch_topk_16(input, offsets, seg_num, seg_len, k, out_vals, out_idx, threads,
+                       half_bits_to_float);
+}
+
+// The same verifier on bfloat16 segments (exact widening to float, the same comparator).
+int oracle_batch_topk_bf16(const uint16_t* input, const int64_t* offsets, int seg_num,
+                           int64_t seg_len, int k, uint16_t* out_vals, int32_t* out_idx,
+                           int threads) {
+  return batch_topk_16(input, offsets, seg_num, seg_len, k, out_vals, out_idx, threads,
+                       bf16_bits_to_float);
 }
 
 // CPU baseline timing: runs the verifier over segments [0, seg_count) `reps` times and

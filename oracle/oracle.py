@@ -1,4 +1,4 @@
-"""Parity oracle for the batched fp16 top-k path (TEST INFRASTRUCTURE ONLY).
+"""Parity oracle for the batched fp16 / bf16 top-k path (TEST INFRASTRUCTURE ONLY).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py``
 may import this module, and only as the checker or as the timed CPU baseline.  The
@@ -28,6 +28,10 @@ How each oracle function is pinned (tests/test_oracle.py):
 * simulate_radix_boundary / select / finalize: the reference's state KATs
   (test/test_batch_topk.cu:66-74, 169-201, 203-234) and a brute-force cumulative count.
 * half <-> float conversions: numpy's float16 casts over every bit pattern.
+* bfloat16 (an extension: the reference covers fp16 only): the bf16 -> float widening
+  against torch's bfloat16 cast over every bit pattern; the bf16 key against float order
+  over every bit pattern and hand-derived known answers; the batched bf16 verifier against
+  the numpy lexsort restatement with the bf16 key on random data with special values.
 * make_random_input: bit patterns are checked against numpy's RNE float16 cast of the
   same floats; the stream itself is libstdc++'s mt19937, as in the reference's tests.
 
@@ -94,6 +98,13 @@ def lib():
         L.oracle_finalize_cutoff_key.argtypes = [vp, ctypes.c_int, vp]
         L.oracle_histogram_pass.restype = None
         L.oracle_histogram_pass.argtypes = [vp, ctypes.c_int, ctypes.c_int, u16, u16, vp]
+        L.oracle_encode_bf16_desc.restype = u16
+        L.oracle_encode_bf16_desc.argtypes = [u16]
+        L.oracle_bf16_to_float_array.restype = None
+        L.oracle_bf16_to_float_array.argtypes = [vp, i64, vp]
+        L.oracle_batch_topk_bf16.restype = ctypes.c_int
+        L.oracle_batch_topk_bf16.argtypes = [vp, vp, ctypes.c_int, i64, ctypes.c_int, vp, vp,
+                                             ctypes.c_int]
         L.oracle_batch_topk_half.restype = ctypes.c_int
         L.oracle_batch_topk_half.argtypes = [vp, vp, ctypes.c_int, i64, ctypes.c_int, vp, vp,
                                              ctypes.c_int]
@@ -122,6 +133,17 @@ def encode_half_asc(bits: int) -> int:
 
 def normalize_half_bits(bits: int) -> int:
     return int(lib().oracle_normalize_half_bits(bits & 0xFFFF))
+
+
+def encode_bf16_desc(bits: int) -> int:
+    return int(lib().oracle_encode_bf16_desc(bits & 0xFFFF))
+
+
+def bf16_to_float(bits: np.ndarray) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, dtype=np.float32)
+    lib().oracle_bf16_to_float_array(_ptr(bits), bits.size, _ptr(out))
+    return out
 
 
 def candidate_better(lhs_bits: int, lhs_index: int, rhs_bits: int, rhs_index: int) -> bool:
@@ -185,11 +207,12 @@ def cutoff_state(bits: np.ndarray, k: int) -> dict:
 
 
 def batch_topk_half(bits: np.ndarray, k: int, seg_len: int | None = None,
-                    offsets: np.ndarray | None = None, threads: int = 1):
+                    offsets: np.ndarray | None = None, threads: int = 1, fmt: str = "f16"):
     """Reference order on every segment -> (values uint16 [S,k], indices int32 [S,k]).
 
     Values are the raw input bits at the selected index; ranks beyond a segment's length
-    are padded with (PAD_VALUE_BITS, PAD_INDEX).
+    are padded with (PAD_VALUE_BITS, PAD_INDEX).  ``fmt`` is "f16" (the reference's format)
+    or "bf16" (the same verifier on bfloat16 bits).
     """
     bits = np.ascontiguousarray(bits, dtype=np.uint16).reshape(-1)
     if offsets is not None:
@@ -203,9 +226,9 @@ def batch_topk_half(bits: np.ndarray, k: int, seg_len: int | None = None,
         sl = seg_len
     vals = np.empty((seg_num, k), dtype=np.uint16)
     idx = np.empty((seg_num, k), dtype=np.int32)
-    rc = lib().oracle_batch_topk_half(_ptr(bits), _ptr(off) if off is not None else None,
-                                      int(seg_num), int(sl), int(k), _ptr(vals), _ptr(idx),
-                                      int(threads))
+    fn = {"f16": lib().oracle_batch_topk_half, "bf16": lib().oracle_batch_topk_bf16}[fmt]
+    rc = fn(_ptr(bits), _ptr(off) if off is not None else None, int(seg_num), int(sl), int(k),
+            _ptr(vals), _ptr(idx), int(threads))
     if rc != 0:
         raise ValueError("oracle rejected the arguments")
     return vals, idx
@@ -248,9 +271,20 @@ def encode_half_desc_np(bits: np.ndarray) -> np.ndarray:
     return key.astype(np.uint16)
 
 
+def encode_bf16_desc_np(bits: np.ndarray) -> np.ndarray:
+    """The same key for bfloat16 bits (inf = 0x7F80; a larger magnitude is a NaN)."""
+    b = np.asarray(bits, dtype=np.uint16).astype(np.uint32)
+    mag = b & 0x7FFF
+    key = np.where((b & 0x8000) != 0, b, b ^ 0x7FFF)
+    key = np.where(mag == 0, 0x7FFF, key)
+    key = np.where(mag > 0x7F80, 0xFFFF, key)
+    return key.astype(np.uint16)
+
+
 def topk_lexsort_np(bits: np.ndarray, k: int, seg_len: int | None = None,
-                    offsets: np.ndarray | None = None):
+                    offsets: np.ndarray | None = None, fmt: str = "f16"):
     """Independent numpy statement of the order: ascending (desc key, index)."""
+    encode = encode_half_desc_np if fmt == "f16" else encode_bf16_desc_np
     bits = np.asarray(bits, dtype=np.uint16).reshape(-1)
     if offsets is None:
         seg_num = bits.size // seg_len
@@ -264,7 +298,7 @@ def topk_lexsort_np(bits: np.ndarray, k: int, seg_len: int | None = None,
         n = seg.size
         if n == 0:
             continue
-        keys = encode_half_desc_np(seg)
+        keys = encode(seg)
         order = np.lexsort((np.arange(n), keys))[:k]
         m = order.size
         idx[s, :m] = order

@@ -31,12 +31,14 @@ def device_u16(bits: np.ndarray, pad_front: int = 0, pad_back: int = 8):
 
 
 def run_fixed(bits: np.ndarray, k: int, poison: int | None = None, elem_offset: int = 0,
-              workspace=None, expect_rc: int = 0):
-    """radix_topk_batch_topk_half on [seg_num, seg_len] bits -> (values u16, indices i32)."""
+              workspace=None, expect_rc: int = 0, fmt: str = "f16"):
+    """radix_topk_batch_topk_{half,bf16} on [seg_num, seg_len] bits -> (values u16, indices i32)."""
     torch = _torch()
     seg_num, seg_len = bits.shape
     buf = device_u16(bits, pad_front=elem_offset)
-    ws_bytes = bt.batch_topk_half_workspace_size(seg_num, seg_len, k)
+    call, ws_size = ((bt.batch_topk_half, bt.batch_topk_half_workspace_size) if fmt == "f16"
+                     else (bt.batch_topk_bf16, bt.batch_topk_bf16_workspace_size))
+    ws_bytes = ws_size(seg_num, seg_len, k)
     assert ws_bytes > 0, (seg_num, seg_len, k)
     if workspace is None:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda:0")
@@ -45,20 +47,23 @@ def run_fixed(bits: np.ndarray, k: int, poison: int | None = None, elem_offset: 
     vals = torch.full((seg_num, k), 0x1234, dtype=torch.int16, device="cuda:0")
     idx = torch.full((seg_num, k), -7, dtype=torch.int32, device="cuda:0")
     stream = torch.cuda.current_stream().cuda_stream
-    rc = bt.batch_topk_half(buf.data_ptr() + 2 * elem_offset, seg_num, seg_len, k,
-                            vals.data_ptr(), idx.data_ptr(), workspace.data_ptr(), ws_bytes, stream)
+    rc = call(buf.data_ptr() + 2 * elem_offset, seg_num, seg_len, k,
+              vals.data_ptr(), idx.data_ptr(), workspace.data_ptr(), ws_bytes, stream)
     assert rc == expect_rc
     torch.cuda.synchronize()
     return vals.cpu().numpy().view(np.uint16), idx.cpu().numpy()
 
 
 def run_segmented(bits: np.ndarray, offsets: np.ndarray, k: int, max_seg_len: int,
-                  poison: int | None = None, elem_offset: int = 0):
+                  poison: int | None = None, elem_offset: int = 0, fmt: str = "f16"):
     torch = _torch()
     seg_num = offsets.size - 1
     buf = device_u16(bits, pad_front=elem_offset)
     off = torch.from_numpy(np.ascontiguousarray(offsets, dtype=np.int32)).to("cuda:0")
-    ws_bytes = bt.batch_topk_half_segmented_workspace_size(seg_num, max_seg_len, k)
+    call, ws_size = ((bt.batch_topk_half_segmented, bt.batch_topk_half_segmented_workspace_size)
+                     if fmt == "f16" else
+                     (bt.batch_topk_bf16_segmented, bt.batch_topk_bf16_segmented_workspace_size))
+    ws_bytes = ws_size(seg_num, max_seg_len, k)
     assert ws_bytes > 0
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda:0")
     if poison is not None:
@@ -66,9 +71,8 @@ def run_segmented(bits: np.ndarray, offsets: np.ndarray, k: int, max_seg_len: in
     vals = torch.full((seg_num, k), 0x1234, dtype=torch.int16, device="cuda:0")
     idx = torch.full((seg_num, k), -7, dtype=torch.int32, device="cuda:0")
     stream = torch.cuda.current_stream().cuda_stream
-    rc = bt.batch_topk_half_segmented(buf.data_ptr() + 2 * elem_offset, off.data_ptr(), seg_num,
-                                      max_seg_len, k, vals.data_ptr(), idx.data_ptr(),
-                                      ws.data_ptr(), ws_bytes, stream)
+    rc = call(buf.data_ptr() + 2 * elem_offset, off.data_ptr(), seg_num, max_seg_len, k,
+              vals.data_ptr(), idx.data_ptr(), ws.data_ptr(), ws_bytes, stream)
     assert rc == 0
     torch.cuda.synchronize()
     return vals.cpu().numpy().view(np.uint16), idx.cpu().numpy()
@@ -85,10 +89,13 @@ def assert_same(got, exp, what: str):
             f"got (idx {gi[s, r]}, bits {gv[s, r]:#06x}) expected (idx {ei[s, r]}, bits {ev[s, r]:#06x})")
 
 
-def assert_properties(bits_rows, vals, idx, k, lengths):
+def assert_properties(bits_rows, vals, idx, k, lengths, fmt: str = "f16"):
     """Size-independent invariants: indices in range and unique, values equal the input at
     the index, keys non-decreasing with ascending index inside equal keys, pads after len."""
-    from oracle.oracle import encode_half_desc_np  # checker only
+    from oracle.oracle import encode_bf16_desc_np, encode_half_desc_np  # checker only
+
+    if fmt != "f16":
+        encode_half_desc_np = encode_bf16_desc_np  # noqa: F811 (same statement, bf16 key)
 
     for s, row in enumerate(bits_rows):
         n = lengths[s]

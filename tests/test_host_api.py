@@ -41,7 +41,9 @@ def test_cpp_dropin_header_forwards_to_c_abi(tmp_path):
     src.write_text('#include "batch_topk.hpp"\n'
                    'size_t f(int a, int b, int c) { return radix_topk::batch_topk_half_workspace_size(a, b, c); }\n'
                    'hipError_t g(const __half* x, __half* v, int* i, void* w, size_t n, hipStream_t s) {\n'
-                   '  return radix_topk::batch_topk_half(x, 1, 8, 3, v, i, w, n, s); }\n')
+                   '  return radix_topk::batch_topk_half(x, 1, 8, 3, v, i, w, n, s); }\n'
+                   'hipError_t h(const __hip_bfloat16* x, __hip_bfloat16* v, int* i, void* w, size_t n,\n'
+                   '             hipStream_t s) { return radix_topk::batch_topk_bf16(x, 1, 8, 3, v, i, w, n, s); }\n')
     res = subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"),
                           "-I", "/opt/rocm/include", "-c", str(src), "-o", str(tmp_path / "use.o")],
                          capture_output=True, text=True)

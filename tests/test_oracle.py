@@ -209,3 +209,68 @@ def test_reference_random_generator_rounds_like_numpy():
     np.testing.assert_array_equal(b, b2)
     _, b3 = O.make_random_input(2, 1000, 7)
     assert not np.array_equal(b, b3)
+
+
+# ------------------------------------------------------------------ bfloat16 extension
+
+BF16_SPECIALS = np.array([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC0, 0xFFC1, 0x7F81, 0x3F80, 0xBF80],
+                         dtype=np.uint16)
+
+
+def test_bf16_widening_matches_torch_exhaustive():
+    torch = pytest.importorskip("torch")
+    bits = np.arange(65536, dtype=np.uint16)
+    ours = O.bf16_to_float(bits)
+    ref = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(ours.view(np.uint32), ref.view(np.uint32))
+
+
+def test_bf16_key_known_answers_and_order():
+    # hand-derived: bf16(1.0) = 0x3F80 -> 0x3F80 ^ 0x7FFF; -1.0 keeps its bits; +-inf, NaN, +-0
+    assert O.encode_bf16_desc(0x3F80) == 0x407F
+    assert O.encode_bf16_desc(0xBF80) == 0xBF80
+    assert O.encode_bf16_desc(0x7F80) == 0x007F and O.encode_bf16_desc(0xFF80) == 0xFF80
+    for nan in (0x7F81, 0x7FC0, 0xFFC1, 0xFFFF):
+        assert O.encode_bf16_desc(nan) == 0xFFFF
+    assert O.encode_bf16_desc(0x0000) == O.encode_bf16_desc(0x8000) == 0x7FFF
+    bits = np.arange(65536, dtype=np.uint16)
+    keys = np.array([O.encode_bf16_desc(int(b)) for b in bits], dtype=np.int64)
+    np.testing.assert_array_equal(keys, O.encode_bf16_desc_np(bits).astype(np.int64))
+    f = (bits.astype(np.uint32) << 16).view(np.float32)
+    nan = np.isnan(f)
+    assert np.all(keys[nan] == 0xFFFF)
+    fv, kv = f[~nan].astype(np.float64), keys[~nan]
+    order = np.argsort(-fv, kind="stable")
+    fs, ks = fv[order], kv[order]
+    assert np.all(np.diff(ks) >= 0)
+    assert np.all((np.diff(ks) == 0) == (np.diff(fs) == 0))
+
+
+def test_bf16_verifier_matches_numpy_lexsort():
+    rng = np.random.default_rng(11)
+    for seg_len, k in [(1, 1), (9, 4), (300, 50), (5000, 256)]:
+        bits = rng.integers(0, 65536, size=5 * seg_len, dtype=np.uint16)
+        bits[rng.random(bits.size) < 0.2] = rng.choice(BF16_SPECIALS, size=1)[0]
+        v1, i1 = O.batch_topk_half(bits, k, seg_len=seg_len, threads=2, fmt="bf16")
+        v2, i2 = O.topk_lexsort_np(bits, k, seg_len=seg_len, fmt="bf16")
+        np.testing.assert_array_equal(i1, i2)
+        np.testing.assert_array_equal(v1, v2)
+
+
+def test_bf16_brute_force_small_rows():
+    alpha = BF16_SPECIALS[:7]
+    for n in range(1, 4):
+        for row in itertools.product(range(len(alpha)), repeat=n):
+            bits = alpha[list(row)]
+            f = (bits.astype(np.uint32) << 16).view(np.float32)
+            # brute force with the reference comparator on floats: NaN last, larger first, index
+            def beats(j, i):
+                if np.isnan(f[j]) != np.isnan(f[i]):
+                    return np.isnan(f[i])
+                if not np.isnan(f[j]) and f[j] != f[i]:
+                    return f[j] > f[i]
+                return j < i
+            rank = [sum(1 for j in range(n) if beats(j, i)) for i in range(n)]
+            for k in range(1, n + 1):
+                _, idx = O.batch_topk_half(bits, k, seg_len=n, fmt="bf16")
+                assert idx[0].tolist() == [rank.index(r) for r in range(k)]

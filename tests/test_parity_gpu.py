@@ -1,5 +1,5 @@
 """GPU parity: the HIP engine, called through the C ABI, against the oracle and the reference
-tests' known answers.  Bit-exact on indices and on the raw fp16 bits of every value."""
+tests' known answers.  Bit-exact on indices and on the raw 16-bit patterns (fp16 or bf16) of every value."""
 
 import json
 import os
@@ -351,3 +351,92 @@ def test_random_segmented_shapes(case):
     got = run_segmented(bits, offsets, k, max_len, elem_offset=elem_offset, poison=0x77)
     exp = O.batch_topk_half(bits, k, offsets=offsets.astype(np.int64), threads=THREADS)
     assert_same(got, exp, f"random segmented case {case}")
+
+
+# ------------------------------------------------------------------ bfloat16 entry points
+
+BF16_SPECIALS = np.array([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC0, 0xFFC1, 0x7F81, 0x3F80, 0xBF80],
+                         dtype=np.uint16)
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    torch = pytest.importorskip("torch")
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).bfloat16().view(torch.int16) \
+        .numpy().view(np.uint16)
+
+
+def check_bf16(bits, k, what, **kw):
+    announce(f"bf16 {what} shape={bits.shape} k={k} {kw}")
+    got = run_fixed(bits, k, fmt="bf16", **kw)
+    exp = O.batch_topk_half(bits, k, seg_len=bits.shape[1], threads=THREADS, fmt="bf16")
+    assert_same(got, exp, f"bf16 {what}")
+    return got
+
+
+@pytest.mark.parametrize("seg_num,seg_len,k", [
+    (16, 4096, 50), (3, 257, 256), (5, 9001, 1), (8, 32000, 128), (4, 131072, 64),
+    (3, 300_000, 50), (2, 200_000, 300), (1, 1_000_000, 1024),
+])
+def test_bf16_random_with_specials(seg_num, seg_len, k):
+    rng = np.random.default_rng(seg_len + k)
+    bits = to_bf16_bits(rng.standard_normal((seg_num, seg_len)) * 3.0)
+    mask = rng.random(bits.shape) < 0.01
+    bits[mask] = BF16_SPECIALS[rng.integers(0, BF16_SPECIALS.size, size=int(mask.sum()))]
+    vals, idx = check_bf16(bits, k, "random with specials")
+    assert_properties(bits, vals, idx, k, [seg_len] * seg_num, fmt="bf16")
+
+
+def test_bf16_llm_logits_full():
+    # The C2 logits (128 x 128,256, N(0, sd 2) with a +8 boosted tail) rounded to bfloat16.
+    bits = to_bf16_bits(wl.llm_logits().view(np.float16).astype(np.float32))
+    vals, idx = check_bf16(bits, 50, "llm_logits")
+    assert_properties(bits, vals, idx, 50, [bits.shape[1]] * bits.shape[0], fmt="bf16")
+
+
+@pytest.mark.parametrize("k", [1, 16, 256])
+def test_bf16_ties_and_specials(k):
+    # 64 distinct values, 1 % -inf, 0.5 % NaN of every encoding, +-0: bit-exact tie order.
+    rng = np.random.default_rng(k)
+    table = to_bf16_bits((np.arange(64) - 32) / 8.0)
+    bits = table[rng.integers(0, 64, size=(32, 20000))]
+    bits[rng.random(bits.shape) < 0.01] = 0xFF80
+    nan_mask = rng.random(bits.shape) < 0.005
+    bits[nan_mask] = np.array([0x7FC0, 0xFFC1, 0x7F81, 0xFFFF], dtype=np.uint16)[
+        rng.integers(0, 4, size=int(nan_mask.sum()))]
+    check_bf16(bits, k, "ties and specials")
+
+
+def test_bf16_top_values_next_to_positive_nans():
+    rng = np.random.default_rng(5)
+    bits = to_bf16_bits(rng.standard_normal((4, 40000)))
+    for r in range(4):
+        top = rng.choice(40000, size=60, replace=False)
+        bits[r, top] = to_bf16_bits(40.0 + rng.integers(0, 8, size=60))
+        bits[r, top ^ 1] = np.array([0x7FC0, 0x7F81, 0x7FFF], dtype=np.uint16)[rng.integers(0, 3, size=60)]
+    check_bf16(bits, 50, "top values beside positive NaNs")
+
+
+def test_bf16_segmented():
+    rng = np.random.default_rng(21)
+    lengths = rng.integers(0, 70000, size=40)
+    lengths[:6] = [0, 1, 7, 49, 64, 65]
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    bits = to_bf16_bits(rng.standard_normal(int(offsets[-1])))
+    announce("bf16 segmented 40 segments k=64")
+    got = run_segmented(bits, offsets, 64, 70000, fmt="bf16")
+    exp = O.batch_topk_half(bits, 64, offsets=offsets, threads=THREADS, fmt="bf16")
+    assert_same(got, exp, "bf16 segmented")
+
+
+def test_bf16_torch_convenience():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(3)
+    bits = to_bf16_bits(rng.standard_normal((6, 5000)))
+    x = torch.from_numpy(bits.view(np.int16)).to("cuda:0").view(torch.bfloat16)
+    announce("bf16 torch topk 6x5000 k=20")
+    vals, idx = bt.topk(x, 20)
+    torch.cuda.synchronize()
+    ev, ei = O.batch_topk_half(bits, 20, seg_len=5000, fmt="bf16")
+    assert vals.dtype == torch.bfloat16
+    assert np.array_equal(idx.cpu().numpy(), ei)
+    assert np.array_equal(vals.view(torch.int16).cpu().numpy().view(np.uint16), ev)
