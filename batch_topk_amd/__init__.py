@@ -36,6 +36,10 @@ EXPORTED_SYMBOLS = (
     "radix_topk_batch_topk_bf16_workspace_size",
     "radix_topk_batch_topk_bf16_segmented",
     "radix_topk_batch_topk_bf16_segmented_workspace_size",
+    "radix_topk_sample_half",
+    "radix_topk_sample_half_workspace_size",
+    "radix_topk_sample_bf16",
+    "radix_topk_sample_bf16_workspace_size",
 )
 
 _lib = None
@@ -74,6 +78,14 @@ def load_library():
         L.radix_topk_batch_topk_bf16_segmented.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, sz, vp]
         L.radix_topk_batch_topk_bf16_segmented_workspace_size.restype = sz
         L.radix_topk_batch_topk_bf16_segmented_workspace_size.argtypes = [i32, i32, i32]
+        f32 = ctypes.c_float
+        for name in ("radix_topk_sample_half", "radix_topk_sample_bf16"):
+            fn = getattr(L, name)
+            fn.restype = i32
+            fn.argtypes = [vp, i32, i32, i32, f32, vp, vp, vp, vp, vp, vp, sz, vp]
+            ws = getattr(L, name + "_workspace_size")
+            ws.restype = sz
+            ws.argtypes = [i32, i32, i32]
         _lib = L
     return _lib
 
@@ -133,6 +145,33 @@ def batch_topk_bf16_segmented(d_input: int, d_offsets: int, seg_num: int, max_se
 def batch_topk_bf16_segmented_workspace_size(seg_num: int, max_seg_len: int, k: int) -> int:
     return int(load_library().radix_topk_batch_topk_bf16_segmented_workspace_size(
         seg_num, max_seg_len, k))
+
+
+def sample_half(d_logits: int, seg_num: int, seg_len: int, k: int, temperature: float,
+                d_uniforms: int, d_topk_values: int, d_topk_indices: int, d_probs: int,
+                d_samples: int, d_workspace: int, workspace_bytes: int, stream: int = 0) -> int:
+    """Top-k sampling over fp16 logits (include/batch_topk.h) -> hipError_t code.
+    ``d_probs`` may be 0 (no probabilities written)."""
+    return int(load_library().radix_topk_sample_half(
+        d_logits, seg_num, seg_len, k, float(temperature), d_uniforms, d_topk_values,
+        d_topk_indices, d_probs or None, d_samples, d_workspace, workspace_bytes, stream))
+
+
+def sample_half_workspace_size(seg_num: int, seg_len: int, k: int) -> int:
+    return int(load_library().radix_topk_sample_half_workspace_size(seg_num, seg_len, k))
+
+
+def sample_bf16(d_logits: int, seg_num: int, seg_len: int, k: int, temperature: float,
+                d_uniforms: int, d_topk_values: int, d_topk_indices: int, d_probs: int,
+                d_samples: int, d_workspace: int, workspace_bytes: int, stream: int = 0) -> int:
+    """Top-k sampling over bfloat16 logits -> hipError_t code."""
+    return int(load_library().radix_topk_sample_bf16(
+        d_logits, seg_num, seg_len, k, float(temperature), d_uniforms, d_topk_values,
+        d_topk_indices, d_probs or None, d_samples, d_workspace, workspace_bytes, stream))
+
+
+def sample_bf16_workspace_size(seg_num: int, seg_len: int, k: int) -> int:
+    return int(load_library().radix_topk_sample_bf16_workspace_size(seg_num, seg_len, k))
 
 
 # ------------------------------------------------------------------ torch conveniences
@@ -209,3 +248,42 @@ def segmented_topk(x, offsets, k: int, max_seg_len: int, workspace=None, stream=
     if rc != HIP_SUCCESS:
         raise TopkError(rc, seg.__name__)
     return vals, idx
+
+
+def sample(logits, k: int, temperature: float, uniforms, with_probs: bool = False,
+           workspace=None, stream=None):
+    """Top-k sampling: one index per row of a contiguous float16 / bfloat16 CUDA tensor
+    [seg_num, seg_len] of logits, drawn from the softmax of the row's top-k at
+    ``temperature`` with ``uniforms`` (float32 CUDA tensor [seg_num], values in [0, 1)).
+
+    Returns (samples int32 [seg_num], top-k values, top-k indices, probs float32
+    [seg_num, k] or None).
+    """
+    import torch
+
+    if logits.dim() != 2 or not logits.is_cuda or not logits.is_contiguous():
+        raise ValueError("sample expects a contiguous 2-D float16 or bfloat16 CUDA tensor")
+    if uniforms.dtype != torch.float32 or not uniforms.is_cuda or uniforms.numel() != logits.shape[0]:
+        raise ValueError("uniforms must be a float32 CUDA tensor with one entry per row")
+    if logits.dtype == torch.float16:
+        fn, ws_size = sample_half, sample_half_workspace_size
+    elif logits.dtype == torch.bfloat16:
+        fn, ws_size = sample_bf16, sample_bf16_workspace_size
+    else:
+        raise ValueError(f"unsupported dtype {logits.dtype}: float16 or bfloat16")
+    seg_num, seg_len = logits.shape
+    ws_bytes = ws_size(seg_num, seg_len, k)
+    if ws_bytes == 0:
+        raise TopkError(HIP_ERROR_INVALID_VALUE, f"{fn.__name__}_workspace_size")
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=logits.device)
+    vals = torch.empty((seg_num, k), dtype=logits.dtype, device=logits.device)
+    idx = torch.empty((seg_num, k), dtype=torch.int32, device=logits.device)
+    probs = torch.empty((seg_num, k), dtype=torch.float32, device=logits.device) if with_probs else None
+    samples = torch.empty(seg_num, dtype=torch.int32, device=logits.device)
+    rc = fn(logits.data_ptr(), seg_num, seg_len, k, temperature, uniforms.data_ptr(), vals.data_ptr(),
+            idx.data_ptr(), probs.data_ptr() if probs is not None else 0, samples.data_ptr(),
+            workspace.data_ptr(), workspace.numel(), _stream_handle(stream))
+    if rc != HIP_SUCCESS:
+        raise TopkError(rc, fn.__name__)
+    return samples, vals, idx, probs

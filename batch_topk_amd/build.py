@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libbatch_topk_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-SOURCES = ["topk_kernels.hip", "api.cpp"]
+SOURCES = ["topk_kernels.hip", "sample_kernels.hip", "api.cpp"]
 
 # -packed-fp32-ops: no v_pk_*_f32 in any code object (this engine has no fp32 math anyway).
 HIP_FLAGS = [
@@ -48,11 +48,11 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
-def resource_usage() -> dict:
+def resource_usage(source: str = "topk_kernels.hip") -> dict:
     """Per-kernel VGPRs, scratch bytes per lane and occupancy (waves per SIMD) of the device
     code, from the compiler's kernel-resource-usage remarks (device-only compile)."""
     cmd = [hipcc(), *HIP_FLAGS, "--cuda-device-only", "-c", "-o", os.devnull,
-           "-Rpass-analysis=kernel-resource-usage", os.path.join(CSRC, "topk_kernels.hip")]
+           "-Rpass-analysis=kernel-resource-usage", os.path.join(CSRC, source)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)

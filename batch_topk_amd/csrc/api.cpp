@@ -10,6 +10,7 @@
 
 #include <atomic>
 #include <chrono>
+#include <cmath>
 #include <cstdint>
 #include <random>
 
@@ -208,6 +209,31 @@ int segmented_topk(uint32_t inf_bits, const uint16_t* d_input, const int32_t* d_
              d_output_indices, d_workspace, workspace_bytes, stream);
 }
 
+// Top-k of every row, then one draw per row from the softmax of its top-k (sampling kernel).
+int sample_topk(bool bf16, const uint16_t* d_logits, int seg_num, int seg_len, int k,
+                float temperature, const float* d_uniforms, uint16_t* d_topk_values,
+                int32_t* d_topk_indices, float* d_probs, int32_t* d_samples, void* d_workspace,
+                size_t workspace_bytes, void* stream) {
+  if (!(temperature > 0.0f) || !std::isfinite(temperature)) return kInvalid;
+  if (!d_uniforms || !d_samples) return kInvalid;
+  const float inv_t = 1.0f / temperature;
+  if (!std::isfinite(inv_t)) return kInvalid;
+  const int rc = fixed_topk(bf16 ? kInfBitsBF16 : kInfBitsF16, d_logits, seg_num, seg_len, k,
+                            d_topk_values, d_topk_indices, d_workspace, workspace_bytes, stream);
+  if (rc != 0) return rc;
+  SampleParams sp{};
+  sp.topk_vals = d_topk_values;
+  sp.topk_idx = d_topk_indices;
+  sp.uniforms = d_uniforms;
+  sp.samples = d_samples;
+  sp.probs = d_probs;
+  sp.inv_temperature = inv_t;
+  sp.seg_num = seg_num;
+  sp.k = k;
+  sp.bf16 = bf16 ? 1 : 0;
+  return launch_topk_sample(sp, stream);
+}
+
 }  // namespace
 }  // namespace radix_topk_amd
 
@@ -264,6 +290,32 @@ int radix_topk_batch_topk_bf16_segmented(const uint16_t* d_input, const int32_t*
   return radix_topk_amd::segmented_topk(kInfBitsBF16, d_input, d_offsets, seg_num, max_seg_len, k,
                                         d_output_values, d_output_indices, d_workspace,
                                         workspace_bytes, stream);
+}
+
+size_t radix_topk_sample_half_workspace_size(int seg_num, int seg_len, int k) {
+  return radix_topk_amd::fixed_workspace_size(seg_num, seg_len, k);
+}
+
+int radix_topk_sample_half(const uint16_t* d_logits, int seg_num, int seg_len, int k,
+                           float temperature, const float* d_uniforms, uint16_t* d_topk_values,
+                           int32_t* d_topk_indices, float* d_probs, int32_t* d_samples,
+                           void* d_workspace, size_t workspace_bytes, void* stream) {
+  return radix_topk_amd::sample_topk(false, d_logits, seg_num, seg_len, k, temperature, d_uniforms,
+                                     d_topk_values, d_topk_indices, d_probs, d_samples, d_workspace,
+                                     workspace_bytes, stream);
+}
+
+size_t radix_topk_sample_bf16_workspace_size(int seg_num, int seg_len, int k) {
+  return radix_topk_amd::fixed_workspace_size(seg_num, seg_len, k);
+}
+
+int radix_topk_sample_bf16(const uint16_t* d_logits, int seg_num, int seg_len, int k,
+                           float temperature, const float* d_uniforms, uint16_t* d_topk_values,
+                           int32_t* d_topk_indices, float* d_probs, int32_t* d_samples,
+                           void* d_workspace, size_t workspace_bytes, void* stream) {
+  return radix_topk_amd::sample_topk(true, d_logits, seg_num, seg_len, k, temperature, d_uniforms,
+                                     d_topk_values, d_topk_indices, d_probs, d_samples, d_workspace,
+                                     workspace_bytes, stream);
 }
 
 }  // extern "C"

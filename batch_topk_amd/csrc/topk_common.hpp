@@ -6,6 +6,9 @@
 
 namespace radix_topk_amd {
 
+// Largest k of every entry point (RADIX_TOPK_MAX_K of the C ABI).
+constexpr int kMaxTopK = 1024;
+
 // LDS entries (8 bytes each) of a workgroup's candidate area: the per-wave candidate regions,
 // then the contiguous candidate list, and for a multi-workgroup segment the merged lists.
 constexpr int kCandArea = 2048;
@@ -112,5 +115,22 @@ struct Plan {
 
 // Device launch of the fused kernel for `plan` (implemented in topk_kernels.hip).
 int launch_segmented_topk(const Plan& plan, const TopkParams& params, void* stream);
+
+// Parameter block of the sampling kernel (sample_kernels.hip): one draw per row from the
+// softmax of the row's top-k values (already written by the top-k kernel, in rank order).
+struct SampleParams {
+  const uint16_t* topk_vals;  // [seg_num, k] raw 16-bit values in rank order
+  const int32_t* topk_idx;    // [seg_num, k] indices; -1 marks ranks past a short segment
+  const float* uniforms;      // [seg_num] u in [0, 1)
+  int32_t* samples;           // [seg_num] sampled index (-1 for an empty segment)
+  float* probs;               // [seg_num, k] or nullptr
+  float inv_temperature;      // 1 / temperature, rounded to fp32
+  int32_t seg_num;
+  int32_t k;
+  int32_t bf16;               // 1: values are bfloat16 bits, 0: fp16
+};
+
+// Device launch of the sampling kernel (implemented in sample_kernels.hip).
+int launch_topk_sample(const SampleParams& params, void* stream);
 
 }  // namespace radix_topk_amd

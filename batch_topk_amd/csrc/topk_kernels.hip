@@ -371,8 +371,6 @@ template <int BLOCK>
 __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int kk, int64_t n,
                                  int seg) {
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wid = tid >> 6;
   if (M < kk) kk = M;  // cannot happen (every candidate list holds >= kk entries); keeps it safe
   for (int r = kk + tid; r < p.k; r += BLOCK) {
     const int64_t o = static_cast<int64_t>(seg) * p.k + r;
@@ -380,8 +378,8 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
     p.out_vals[o] = 0xffffu;
   }
   constexpr int NW = BLOCK / 64;
-  // Small sets: every wave ranks its share against the whole list held in registers and
-  // writes the output entries of its candidates that rank below kk.
+  // Small sets: one DPP row per candidate counts the smaller entries (row_rank_write); up to
+  // 512: every wave ranks its share against the whole list held in registers.
   if (M <= 128) {
     row_rank_write<BLOCK>(p, n, seg, sm.area, M, kk);
     return;

@@ -18,7 +18,9 @@ Prints ONE JSON line:
 Other workloads (--workload uniform_small | ties_special | varlen | huge_segment, and
 ref_matrix --seg-num N for the reference's own benchmark matrix) print the same line for
 that configuration.  --dtype bf16 runs the bfloat16 entry points on the same workload
-rounded to bfloat16 (no CPU baseline: that is the reference's fp16 verifier).
+rounded to bfloat16 (no CPU baseline: that is the reference's fp16 verifier).  --op sample
+times the top-k sampling consumer (radix_topk_sample_*: the top-k, then one draw per row
+from the softmax of its top-k at --temperature) on fixed-length workloads.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--k K] [--dtype f16|bf16]
 """
@@ -86,6 +88,10 @@ def load_traffic(workload: str, k: int):
     return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
+def offsets_of(workload: str) -> bool:
+    return workload == "varlen"
+
+
 def cpu_baseline(bits: np.ndarray, k: int, threads: int):
     """Reference host verifier over the whole batch, serial (threads=1) and threaded."""
     from oracle import oracle as O  # the checker, timed as the CPU baseline only
@@ -121,6 +127,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--dtype", choices=("f16", "bf16"), default="f16")
+    ap.add_argument("--op", choices=("topk", "sample"), default="topk")
+    ap.add_argument("--temperature", type=float, default=1.0)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the engine has no "
@@ -135,6 +143,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     bits, offsets, cfg = make_input(args.workload, args.seg_num)
     k = args.k
+    if args.op == "sample" and offsets_of(args.workload):
+        raise SystemExit("--op sample runs on fixed-length workloads")
     if args.dtype == "bf16":
         # the same workload rounded to bfloat16 (round to nearest even)
         bits = torch.from_numpy(bits.view(np.float16).astype(np.float32)).bfloat16() \
@@ -166,9 +176,17 @@ def main() -> int:
     idx = torch.empty((seg_num, k), dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
+    if args.op == "sample":
+        sample_fn = bt.sample_half if args.dtype == "f16" else bt.sample_bf16
+        uniforms = torch.rand(seg_num, dtype=torch.float32, device=dev, generator=torch.Generator(dev).manual_seed(0))
+        samples = torch.empty(seg_num, dtype=torch.int32, device=dev)
 
     def call(i: int) -> None:
-        if offsets is None:
+        if args.op == "sample":
+            rc = sample_fn(inputs[i % copies].data_ptr(), seg_num, seg_len, k, args.temperature,
+                           uniforms.data_ptr(), vals.data_ptr(), idx.data_ptr(), 0, samples.data_ptr(),
+                           ws.data_ptr(), ws_bytes, sh)
+        elif offsets is None:
             rc = fixed(inputs[i % copies].data_ptr(), seg_num, seg_len, k, vals.data_ptr(),
                        idx.data_ptr(), ws.data_ptr(), ws_bytes, sh)
         else:
@@ -227,14 +245,17 @@ def main() -> int:
     # Algorithmic bytes: every input element read once (2 B), every output rank written once
     # (2 B value + 4 B index), plus the offsets array when given.
     alg_bytes = 2 * n_elements + 6 * seg_num * k + (0 if offsets is None else 4 * (seg_num + 1))
+    if args.op == "sample":
+        alg_bytes += 8 * seg_num  # one uniform in, one sampled index out per row
     # The kernel's average launch duration over the timed region (back-to-back launches,
     # events on the launch stream).
     step_us = ms_per_step * 1e3
     achieved = alg_bytes / (step_us * 1e-6)
     value = seg_num * steps / (total_ms * 1e-3)
     dname = "fp16" if args.dtype == "f16" else "bf16"
-    metric = METRIC if (args.workload == "llm_logits" and k == 50 and args.dtype == "f16") else \
-        f"segments/s and achieved HBM GB/s, {dname} top-{k} over {cfg['workload'].split(':')[0]}"
+    metric = METRIC if (args.workload == "llm_logits" and k == 50 and args.dtype == "f16" and args.op == "topk") else \
+        f"segments/s and achieved HBM GB/s, {dname} top-{k}{' sampling' if args.op == 'sample' else ''} " \
+        f"over {cfg['workload'].split(':')[0]}"
     result = {
         "metric": metric,
         "value": value,
@@ -248,14 +269,16 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "u16" if args.dtype == "f16" else "u16 (bf16 keys)",
         "data": "synthetic",
-        "config": dict(cfg, k=k, input_copies=copies, parallelism="single GPU"),
+        "config": dict(cfg, k=k, input_copies=copies, parallelism="single GPU",
+                       **({"op": "top-k sampling", "temperature": args.temperature} if args.op == "sample" else {})),
         "roofline": {
             "bound": "hbm",
             "achieved": achieved / 1e9,
             "peak": HBM_PEAK_BPS / 1e9,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_BPS,
-            "traffic": load_traffic(args.workload if args.dtype == "f16" else f"{args.workload}:bf16", k),
+            "traffic": load_traffic(args.workload if args.dtype == "f16" else f"{args.workload}:bf16", k)
+            if args.op == "topk" else None,
         },
         "elements_per_s": n_elements * steps / (total_ms * 1e-3),
         "hbm_gbps_whole_job": alg_bytes * steps / (total_ms * 1e-3) / 1e9,
@@ -271,7 +294,7 @@ def main() -> int:
         target = REF_MATRIX_TARGET_US.get((seg_num, seg_len, k))
         result["reference_target_us_rtx4080"] = target
         result["target_over_measured"] = None if target is None else target / (ms_per_step * 1e3)
-    if not args.no_cpu_baseline and offsets is None and args.dtype == "f16":
+    if not args.no_cpu_baseline and offsets is None and args.dtype == "f16" and args.op == "topk":
         log("timing the CPU baseline (reference host verifier)...")
         t0 = time.time()
         result["cpu_baseline"] = cpu_baseline(bits, k, args.cpu_threads)

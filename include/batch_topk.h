@@ -104,6 +104,36 @@ int radix_topk_batch_topk_bf16_segmented(const uint16_t* d_input, const int32_t*
                                          void* stream);
 size_t radix_topk_batch_topk_bf16_segmented_workspace_size(int seg_num, int max_seg_len, int k);
 
+/*
+ * Top-k sampling (LLM decoding): the top-k of every row exactly as radix_topk_batch_topk_half
+ * (written to d_topk_values / d_topk_indices), then one index drawn per row from the softmax
+ * of its top-k at the given temperature, using the caller's uniform d_uniforms[row] in [0, 1).
+ * With v_0 >= v_1 >= ... the row's top-k values in output order (as floats) and m the number
+ * of ranks with an index >= 0:
+ *   w_0 = 1; for r >= 1, w_r = 1 if v_r == v_0, else exp((v_r - v_0) * (1 / temperature))
+ *   (1 / temperature rounded to float), and 0 where that is NaN;
+ *   S = w_0 + ... + w_{m-1};  d_samples[row] = the index at the first rank r whose running
+ *   sum w_0 + ... + w_r exceeds u * S (the last rank if rounding leaves none);
+ *   d_probs[row * k + r] = w_r / S (0 past m), when d_probs is not NULL.
+ * Sums are in fp32, so probabilities carry fp32 rounding; the top-k itself is bit-exact.
+ * Rejected (-> 1): everything batch_topk_half rejects, temperature not finite or <= 0,
+ * NULL d_uniforms or d_samples.  Workspace: radix_topk_sample_half_workspace_size (equal to
+ * the top-k's).  Two launches on `stream`, nothing allocated.
+ * No counterpart in the reference; it is the consumer the reference's LLM-sampling workload
+ * (128 x 128,256 logits, k = 50) feeds.
+ */
+int radix_topk_sample_half(const uint16_t* d_logits, int seg_num, int seg_len, int k,
+                           float temperature, const float* d_uniforms, uint16_t* d_topk_values,
+                           int32_t* d_topk_indices, float* d_probs, int32_t* d_samples,
+                           void* d_workspace, size_t workspace_bytes, void* stream);
+size_t radix_topk_sample_half_workspace_size(int seg_num, int seg_len, int k);
+/* The same for bfloat16 logits (top-k as radix_topk_batch_topk_bf16). */
+int radix_topk_sample_bf16(const uint16_t* d_logits, int seg_num, int seg_len, int k,
+                           float temperature, const float* d_uniforms, uint16_t* d_topk_values,
+                           int32_t* d_topk_indices, float* d_probs, int32_t* d_samples,
+                           void* d_workspace, size_t workspace_bytes, void* stream);
+size_t radix_topk_sample_bf16_workspace_size(int seg_num, int seg_len, int k);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -32,6 +32,11 @@ How each oracle function is pinned (tests/test_oracle.py):
   against torch's bfloat16 cast over every bit pattern; the bf16 key against float order
   over every bit pattern and hand-derived known answers; the batched bf16 verifier against
   the numpy lexsort restatement with the bf16 key on random data with special values.
+* sample_topk_np (the sampling consumer, an extension with no reference counterpart): the
+  softmax weights against scipy.special.softmax, closed forms (k = 1, equal logits, the
+  two-value logistic), and a deterministic grid of uniforms whose sampled-rank histogram
+  must equal the probabilities times the grid size.  It is floating point: GPU results are
+  compared to it with the tolerances stated in tests/test_sample_gpu.py.
 * make_random_input: bit patterns are checked against numpy's RNE float16 cast of the
   same floats; the stream itself is libstdc++'s mt19937, as in the reference's tests.
 
@@ -304,3 +309,54 @@ def topk_lexsort_np(bits: np.ndarray, k: int, seg_len: int | None = None,
         idx[s, :m] = order
         vals[s, :m] = seg[order]
     return vals, idx
+
+
+# ---------------------------------------------------------------- sampling consumer
+
+def bits_to_float64(bits: np.ndarray, fmt: str = "f16") -> np.ndarray:
+    """Exact widening of fp16 / bfloat16 bit patterns to float64."""
+    b = np.asarray(bits, dtype=np.uint16)
+    if fmt == "f16":
+        return b.view(np.float16).astype(np.float64)
+    return (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def sample_topk_np(vals_bits: np.ndarray, idx: np.ndarray, temperature: float,
+                   uniforms: np.ndarray, fmt: str = "f16"):
+    """The sampling rule of include/batch_topk.h (radix_topk_sample_*), in float64, on a top-k
+    output [S, k] (values in rank order, indices with -1 past a short segment).
+
+    -> (samples int32 [S], probs float64 [S, k], cumulative sums float64 [S, k], totals [S]).
+    1 / temperature is rounded to float32 first, as the library does on the host.
+    """
+    v = bits_to_float64(vals_bits, fmt)
+    idx = np.asarray(idx)
+    inv_t = float(np.float32(1.0) / np.float32(temperature))
+    S, k = v.shape
+    samples = np.full(S, -1, dtype=np.int32)
+    probs = np.zeros((S, k))
+    cums = np.zeros((S, k))
+    totals = np.zeros(S)
+    for s in range(S):
+        m = int(np.sum(idx[s] >= 0))
+        if m == 0:
+            continue
+        w = np.zeros(k)
+        w[0] = 1.0
+        with np.errstate(invalid="ignore", over="ignore"):
+            for r in range(1, m):
+                if v[s, r] == v[s, 0]:
+                    w[r] = 1.0
+                else:
+                    x = np.exp((v[s, r] - v[s, 0]) * inv_t)
+                    w[r] = 0.0 if np.isnan(x) else x
+        c = np.cumsum(w)
+        total = c[m - 1]
+        target = float(uniforms[s]) * total
+        hits = np.nonzero(c[:m] > target)[0]
+        r = int(hits[0]) if hits.size else m - 1
+        samples[s] = idx[s, r]
+        probs[s] = w / total
+        cums[s] = c
+        totals[s] = total
+    return samples, probs, cums, totals

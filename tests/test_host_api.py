@@ -129,3 +129,20 @@ def test_kernel_resources_keep_occupancy_without_spills():
     for name, r in kernels.items():
         assert r["ScratchSize [bytes/lane]"] == 0, (name, r)
         assert r["Occupancy [waves/SIMD]"] >= 4, (name, r)
+
+
+def test_sample_validation_rejects_before_any_hip_call():
+    ws = bt.sample_half_workspace_size(2, 1000, 50)
+    assert ws == bt.batch_topk_half_workspace_size(2, 1000, 50) > 1
+    assert bt.sample_bf16_workspace_size(2, 1000, 50) == ws
+    P_U, P_S, P_PR = 0x60000, 0x70000, 0x80000
+    for fn in (bt.sample_half, bt.sample_bf16):
+        ok = dict(d_logits=P_IN, seg_num=2, seg_len=1000, k=50, temperature=1.0, d_uniforms=P_U,
+                  d_topk_values=P_VAL, d_topk_indices=P_IDX, d_probs=P_PR, d_samples=P_S,
+                  d_workspace=P_WS, workspace_bytes=ws)
+        for bad in (dict(temperature=0.0), dict(temperature=-1.0), dict(temperature=float("nan")),
+                    dict(temperature=float("inf")), dict(temperature=1e-45),
+                    dict(d_uniforms=0), dict(d_samples=0), dict(d_logits=0), dict(d_topk_values=0),
+                    dict(d_topk_indices=0), dict(d_workspace=0), dict(k=0), dict(k=1001),
+                    dict(seg_num=0), dict(workspace_bytes=ws - 1)):
+            assert fn(**dict(ok, **bad)) == INVALID, (fn.__name__, bad)

@@ -274,3 +274,54 @@ def test_bf16_brute_force_small_rows():
             for k in range(1, n + 1):
                 _, idx = O.batch_topk_half(bits, k, seg_len=n, fmt="bf16")
                 assert idx[0].tolist() == [rank.index(r) for r in range(k)]
+
+
+# ------------------------------------------------------------------ sampling consumer
+
+def test_sample_rule_matches_scipy_softmax():
+    special = pytest.importorskip("scipy.special")
+    rng = np.random.default_rng(4)
+    k = 50
+    logits = np.sort(rng.standard_normal((8, k)) * 3, axis=1)[:, ::-1].astype(np.float16)
+    bits = logits.view(np.uint16)
+    idx = np.tile(np.arange(k, dtype=np.int32), (8, 1))
+    for temp in (0.25, 1.0, 3.0):
+        _, probs, _, _ = O.sample_topk_np(bits, idx, temp, np.full(8, 0.5))
+        inv_t = float(np.float32(1.0) / np.float32(temp))
+        ref = special.softmax(logits.astype(np.float64) * inv_t, axis=1)
+        np.testing.assert_allclose(probs, ref, rtol=1e-12, atol=1e-15)
+
+
+def test_sample_rule_closed_forms():
+    # k = 1: the only candidate, whatever u
+    s, p, _, _ = O.sample_topk_np(np.array([[0x3C00]], np.uint16), np.array([[7]]), 1.0, np.array([0.999]))
+    assert s[0] == 7 and p[0, 0] == 1.0
+    # equal logits: uniform; u in the j-th 1/m slice picks rank j
+    m = 8
+    bits = np.full((1, m), 0x4000, np.uint16)
+    idx = np.arange(m, dtype=np.int32)[None, :] + 100
+    for j in range(m):
+        s, p, _, _ = O.sample_topk_np(bits, idx, 0.7, np.array([(j + 0.5) / m]))
+        assert s[0] == 100 + j
+        np.testing.assert_allclose(p[0], 1.0 / m)
+    # two values d apart: p0 = 1 / (1 + exp(-d / T))
+    bits = np.array([[np.float16(2.0).view(np.uint16), np.float16(0.5).view(np.uint16)]])
+    _, p, _, _ = O.sample_topk_np(bits, np.array([[0, 1]]), 0.5, np.array([0.1]))
+    assert abs(p[0, 0] - 1.0 / (1.0 + np.exp(-1.5 / 0.5))) < 1e-12
+    # NaN logits get weight 0, -inf gets 0 below a finite best, pads are skipped
+    nan, ninf = 0x7E00, 0xFC00
+    bits = np.array([[0x3C00, ninf, nan, 0xFFFF]], np.uint16)
+    _, p, _, _ = O.sample_topk_np(bits, np.array([[3, 4, 5, -1]]), 1.0, np.array([0.99]))
+    assert p[0].tolist() == [1.0, 0.0, 0.0, 0.0]
+
+
+def test_sample_rule_histogram_on_a_uniform_grid():
+    rng = np.random.default_rng(9)
+    k, n = 20, 4000
+    logits = np.sort(rng.standard_normal(k), kind="stable")[::-1].astype(np.float16)
+    bits = np.tile(logits.view(np.uint16), (n, 1))
+    idx = np.tile(np.arange(k, dtype=np.int32), (n, 1))
+    u = (np.arange(n) + 0.5) / n
+    s, p, _, _ = O.sample_topk_np(bits, idx, 1.3, u)
+    counts = np.bincount(s, minlength=k)
+    assert np.all(np.abs(counts - n * p[0]) <= 1.0 + 1e-9)
