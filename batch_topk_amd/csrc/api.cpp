@@ -136,9 +136,17 @@ uint64_t next_epoch() {
   }
 }
 
+// Top-k sampling request riding on a top-k call (sample_topk).
+struct SampleSpec {
+  const float* uniforms;
+  int32_t* samples;
+  float* probs;
+  float inv_temperature;
+};
+
 int run(const Plan& plan, uint32_t inf_bits, const uint16_t* d_input, const int32_t* d_offsets,
         int seg_num, int64_t seg_len, int64_t max_len, int k, uint16_t* d_values, int32_t* d_indices,
-        void* d_workspace, size_t workspace_bytes, void* stream) {
+        void* d_workspace, size_t workspace_bytes, void* stream, const SampleSpec* sample = nullptr) {
   if (!plan.ok || workspace_bytes < plan.ws_bytes) return kInvalid;
   const uintptr_t in_addr = reinterpret_cast<uintptr_t>(d_input);
   if ((in_addr & 1u) || (reinterpret_cast<uintptr_t>(d_values) & 1u) ||
@@ -174,7 +182,27 @@ int run(const Plan& plan, uint32_t inf_bits, const uint16_t* d_input, const int3
   }
   p.epoch = next_epoch();
   p.inf_bits = inf_bits;
-  return launch_segmented_topk(plan, p, stream);
+  // Sampling is fused into the kernel's last step, except on a cooperative plan (the ranking
+  // is spread over the segment's workgroups): there a one-wave-per-row kernel follows.
+  if (sample && !plan.cooperative) {
+    p.uniforms = sample->uniforms;
+    p.samples = sample->samples;
+    p.probs = sample->probs;
+    p.inv_temperature = sample->inv_temperature;
+  }
+  const int rc = launch_segmented_topk(plan, p, stream);
+  if (rc != 0 || !sample || !plan.cooperative) return rc;
+  SampleParams sp{};
+  sp.topk_vals = d_values;
+  sp.topk_idx = d_indices;
+  sp.uniforms = sample->uniforms;
+  sp.samples = sample->samples;
+  sp.probs = sample->probs;
+  sp.inv_temperature = sample->inv_temperature;
+  sp.seg_num = seg_num;
+  sp.k = k;
+  sp.bf16 = inf_bits == kInfBitsBF16 ? 1 : 0;
+  return launch_topk_sample(sp, stream);
 }
 
 size_t fixed_workspace_size(int seg_num, int seg_len, int k) {
@@ -209,29 +237,21 @@ int segmented_topk(uint32_t inf_bits, const uint16_t* d_input, const int32_t* d_
              d_output_indices, d_workspace, workspace_bytes, stream);
 }
 
-// Top-k of every row, then one draw per row from the softmax of its top-k (sampling kernel).
+// Top-k of every row, then one draw per row from the softmax of its top-k.
 int sample_topk(bool bf16, const uint16_t* d_logits, int seg_num, int seg_len, int k,
                 float temperature, const float* d_uniforms, uint16_t* d_topk_values,
                 int32_t* d_topk_indices, float* d_probs, int32_t* d_samples, void* d_workspace,
                 size_t workspace_bytes, void* stream) {
+  if (seg_num <= 0 || seg_len <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K || k > seg_len) return kInvalid;
+  if (!d_logits || !d_topk_values || !d_topk_indices || !d_workspace) return kInvalid;
   if (!(temperature > 0.0f) || !std::isfinite(temperature)) return kInvalid;
   if (!d_uniforms || !d_samples) return kInvalid;
   const float inv_t = 1.0f / temperature;
   if (!std::isfinite(inv_t)) return kInvalid;
-  const int rc = fixed_topk(bf16 ? kInfBitsBF16 : kInfBitsF16, d_logits, seg_num, seg_len, k,
-                            d_topk_values, d_topk_indices, d_workspace, workspace_bytes, stream);
-  if (rc != 0) return rc;
-  SampleParams sp{};
-  sp.topk_vals = d_topk_values;
-  sp.topk_idx = d_topk_indices;
-  sp.uniforms = d_uniforms;
-  sp.samples = d_samples;
-  sp.probs = d_probs;
-  sp.inv_temperature = inv_t;
-  sp.seg_num = seg_num;
-  sp.k = k;
-  sp.bf16 = bf16 ? 1 : 0;
-  return launch_topk_sample(sp, stream);
+  const Plan plan = make_plan(seg_num, seg_len, k);
+  const SampleSpec spec{d_uniforms, d_samples, d_probs, inv_t};
+  return run(plan, bf16 ? kInfBitsBF16 : kInfBitsF16, d_logits, nullptr, seg_num, seg_len, seg_len, k,
+             d_topk_values, d_topk_indices, d_workspace, workspace_bytes, stream, &spec);
 }
 
 }  // namespace

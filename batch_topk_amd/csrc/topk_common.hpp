@@ -89,6 +89,11 @@ struct TopkParams {
   unsigned long long* lists;    // [seg_num * W * cap_list] packed (key16 << 32 | index)
   unsigned long long epoch;     // 48-bit token unique to this call
   uint32_t inf_bits;            // +inf pattern of the 16-bit element format (0x7C00 fp16, 0x7F80 bf16)
+  // Top-k sampling fused into the last step (non-cooperative plans), off when samples is null.
+  const float* uniforms;        // [seg_num] u in [0, 1)
+  int32_t* samples;             // [seg_num] sampled index (-1 for an empty segment)
+  float* probs;                 // [seg_num, k] or nullptr
+  float inv_temperature;        // 1 / temperature, rounded to fp32
   unsigned char* groups;        // cooperative path: [seg_num] blocks of group_layout(W).bytes
 };
 

@@ -47,6 +47,7 @@
 #include <cstdint>
 #include <cstdlib>
 
+#include "sample_row.hpp"
 #include "topk_common.hpp"
 
 // Phase timestamp hook for profiling builds; compiled out otherwise.
@@ -298,7 +299,7 @@ __device__ void block_rank(const u64* v, int M, int* rank) {
 // share of the candidates with ballots: rank(x) = sum over slots of popcount(ballot(c < x)).
 template <int BLOCK, int S>
 __device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
-                                int kk) {
+                                int kk, u64* sorted) {
   constexpr int NW = BLOCK / 64;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -331,15 +332,20 @@ __device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u
     my_rank = lane == t ? r : my_rank;
   }
   TOPK_WTRACE(7);
-  if (lane < count && my_rank < kk) write_rank(p, n, seg, my_rank, mine);
+  if (lane < count && my_rank < kk) {
+    write_rank(p, n, seg, my_rank, mine);
+    if (sorted) sorted[my_rank] = mine;
+  }
 }
 
-// Ranks the M (<= 128) unique candidates of `list` and writes those of rank < kk.  One DPP
+// Ranks the M (<= 128) unique candidates of `list` and writes those of rank < kk (also to
+// sorted[rank] when sorted is not null).  One DPP
 // row (16 lanes) per candidate: lane q of the row compares it with entries q, q + 16, ... (held
 // in registers, loaded once), and a row prefix sum leaves its rank in the row's last lane,
 // which writes the output entry.  The rows take the candidates in turn.
 template <int BLOCK>
-__device__ void row_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M, int kk) {
+__device__ void row_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M, int kk,
+                               u64* sorted) {
   constexpr int ROWS = BLOCK / 16;
   const int row = threadIdx.x >> 4;
   const int q = threadIdx.x & 15;
@@ -360,13 +366,31 @@ __device__ void row_rank_write(const TopkParams& p, int64_t n, int seg, const u6
     cnt += dpp<0x112, 0xf>(cnt);
     cnt += dpp<0x114, 0xf>(cnt);
     cnt += dpp<0x118, 0xf>(cnt);
-    if (q == 15 && cnt < static_cast<u32>(kk)) write_rank(p, n, seg, static_cast<int>(cnt), x);
+    if (q == 15 && cnt < static_cast<u32>(kk)) {
+      write_rank(p, n, seg, static_cast<int>(cnt), x);
+      if (sorted) sorted[cnt] = x;
+    }
   }
   TOPK_WTRACE(7);
 }
 
+// Writes the top-k sampling draw of segment `seg` from its ranked entries sorted[0..kk)
+// (wave 0), or the empty-row draw when kk is 0.  Only called when p.samples is set.
+__device__ __forceinline__ void sample_segment(const TopkParams& p, const u64* sorted, int kk, int seg) {
+  if (threadIdx.x >= 64) return;
+  const bool bf16 = p.inf_bits == kInfBitsBF16;
+  auto get = [&](int r) {
+    const u64 P = sorted[r];
+    return RankedEntry{bits16_to_float(cand_raw(P), bf16), static_cast<int32_t>(cand_index(P))};
+  };
+  sample_ranked_row(get, kk, p.k, p.inv_temperature, p.uniforms[seg], p.samples + seg,
+                    p.probs ? p.probs + static_cast<int64_t>(seg) * p.k : nullptr);
+}
+
 // Select the kk best of the M packed candidates in `sm.area` (M >= kk) and write them, in
 // order, to the segment's output row; ranks kk..k-1 get the pad (index -1, bits 0xFFFF).
+// With top-k sampling on, the ranked entries are also kept in LDS (sm.sel, or sm.area when
+// sm.sel holds the selection) and wave 0 then draws the segment's sample.
 template <int BLOCK>
 __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int kk, int64_t n,
                                  int seg) {
@@ -377,36 +401,42 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
     p.out_idx[o] = -1;
     p.out_vals[o] = 0xffffu;
   }
+  const bool sampling = p.samples != nullptr;
   constexpr int NW = BLOCK / 64;
+  u64* sorted = sm.sel;
   // Small sets: one DPP row per candidate counts the smaller entries (row_rank_write); up to
   // 512: every wave ranks its share against the whole list held in registers.
   if (M <= 128) {
-    row_rank_write<BLOCK>(p, n, seg, sm.area, M, kk);
-    return;
-  }
-  if constexpr (NW >= 8) {
-    if (M <= 8 * NW * 4 && M <= 512) {
-      wave_rank_write<BLOCK, 8>(p, n, seg, sm.area, M, kk);
-      return;
-    }
-  }
-  const u64* sel = sm.area;
-  if (M > kk) {
-    const u64 bound = block_select_bound<BLOCK>(sm.area, M, kk, sm.hist, sm.scal);
-    if (tid == 0) sm.scal[3] = 0;
-    __syncthreads();
-    for (int i = tid; i < M; i += BLOCK) {
-      const u64 P = sm.area[i];
-      if (P <= bound) {
-        const int slot = atomicAdd(&sm.scal[3], 1);
-        if (slot < p.kpad) sm.sel[slot] = P;
+    row_rank_write<BLOCK>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+  } else if (NW >= 8 && M <= 8 * NW * 4 && M <= 512) {
+    if constexpr (NW >= 8) wave_rank_write<BLOCK, 8>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+  } else {
+    const u64* sel = sm.area;
+    if (M > kk) {
+      const u64 bound = block_select_bound<BLOCK>(sm.area, M, kk, sm.hist, sm.scal);
+      if (tid == 0) sm.scal[3] = 0;
+      __syncthreads();
+      for (int i = tid; i < M; i += BLOCK) {
+        const u64 P = sm.area[i];
+        if (P <= bound) {
+          const int slot = atomicAdd(&sm.scal[3], 1);
+          if (slot < p.kpad) sm.sel[slot] = P;
+        }
       }
+      __syncthreads();
+      sel = sm.sel;
+      sorted = sm.area;  // the candidates are no longer needed
     }
-    __syncthreads();
-    sel = sm.sel;
+    block_rank<BLOCK>(sel, kk, sm.rank);
+    for (int i = tid; i < kk; i += BLOCK) {
+      write_rank(p, n, seg, sm.rank[i], sel[i]);
+      if (sampling) sorted[sm.rank[i]] = sel[i];
+    }
   }
-  block_rank<BLOCK>(sel, kk, sm.rank);
-  for (int i = tid; i < kk; i += BLOCK) write_rank(p, n, seg, sm.rank[i], sel[i]);
+  if (sampling) {
+    __syncthreads();
+    sample_segment(p, sorted, kk, seg);
+  }
 }
 
 // Epoch-tagged arrival counter: word = epoch << 16 | count.  A word carrying another epoch
@@ -708,6 +738,7 @@ segmented_topk_kernel(TopkParams p) {
         p.out_idx[o] = -1;
         p.out_vals[o] = 0xffffu;
       }
+      if (!COOP && p.samples) sample_segment(p, nullptr, 0, seg);
     }
     return;
   }

@@ -148,3 +148,13 @@ def test_sample_without_probs_and_torch_convenience():
         target = float(u[s]) * tot[s]
         if np.min(np.abs(cum[s, :20] - target)) > SAMPLE_RTOL * tot[s]:
             assert got[s] == es[s]
+
+
+@pytest.mark.parametrize("seg_num,seg_len,k", [
+    (3, 300_000, 50),     # several workgroups per row, the last one merges and samples
+    (2, 600_000, 512),    # cooperative plan: the stand-alone sampling kernel follows
+])
+def test_sample_multi_workgroup_plans(seg_num, seg_len, k):
+    rng = np.random.default_rng(seg_len + k)
+    bits = (rng.standard_normal((seg_num, seg_len)) * 2).astype(np.float16).view(np.uint16)
+    check_sample(bits, k, 1.0, rng.random(seg_num), f"multi-workgroup {seg_num}x{seg_len}")
