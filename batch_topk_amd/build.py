@@ -17,6 +17,10 @@ LIB_NAME = "libbatch_topk_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
 SOURCES = ["topk_kernels.hip", "sample_kernels.hip", "api.cpp"]
+# Measurement reference (not part of the engine): the single-pass read floor, loaded by
+# batch_topk_amd/profiling.py only.
+FLOOR_LIB_PATH = os.path.join(HERE, "libread_floor.so")
+FLOOR_SOURCES = ["read_floor.hip"]
 
 # -packed-fp32-ops: no v_pk_*_f32 in any code object (this engine has no fp32 math anyway).
 HIP_FLAGS = [
@@ -33,18 +37,24 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> str:
-    """Always recompiles (the build check must exercise the compiler)."""
-    tmp = LIB_PATH + ".tmp"
+def _compile(sources, out_path: str, verbose: bool) -> None:
+    tmp = out_path + ".tmp"
     cmd = [hipcc(), *HIP_FLAGS, "-shared", "-o", tmp,
-           *[os.path.join(CSRC, s) for s in SOURCES], "-lamdhip64"]
+           *[os.path.join(CSRC, s) for s in sources], "-lamdhip64"]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed to build " + LIB_NAME)
-    os.replace(tmp, LIB_PATH)
+        raise RuntimeError("hipcc failed to build " + os.path.basename(out_path))
+    os.replace(tmp, out_path)
+
+
+def build(verbose: bool = False) -> str:
+    """Always recompiles (the build check must exercise the compiler): the engine library and
+    the read-floor measurement library."""
+    _compile(SOURCES, LIB_PATH, verbose)
+    _compile(FLOOR_SOURCES, FLOOR_LIB_PATH, verbose)
     return LIB_PATH
 
 

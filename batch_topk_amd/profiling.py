@@ -16,6 +16,14 @@
       HBM bytes per launch of the top-k kernel: its FETCH_SIZE and WRITE_SIZE (KiB per
       dispatch), each scaled by known bytes / measured KiB of the copy kernel, merged into the
       JSON table bench.py reads.
+
+  python -m batch_topk_amd.profiling floor [--calls 2000]
+      Back-to-back time of the single-pass read floor (libread_floor.so) over the 128 x 128,256
+      fp16 batch, rotating over 17 input copies (557 MB), for several workgroup shapes.
+
+  python -m batch_topk_amd.profiling matrix [--out FILE]
+      bench.py over every workload (fp16, plus bf16 and the sampling consumer on the LLM
+      logits), as a markdown table.
 """
 
 from __future__ import annotations
@@ -62,6 +70,101 @@ def run_copy(mib: int, reps: int) -> None:
     print(f"copy: {reps} dispatches reading and writing {mib} MiB each")
 
 
+FLOOR_SHAPES = ((1024, 16, 1), (512, 32, 1), (512, 16, 2), (1024, 8, 2), (256, 16, 4))
+
+
+def run_floor(calls: int) -> None:
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from batch_topk_amd import build, workloads
+
+    lib = ctypes.CDLL(build.FLOOR_LIB_PATH)
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    lib.read_floor_run.restype = i32
+    lib.read_floor_run.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, vp]
+    bits = workloads.llm_logits()
+    rows, row_len = bits.shape
+    src = torch.from_numpy(bits.view(np.int16)).to("cuda:0")
+    copies = [src] + [src.clone() for _ in range(16)]
+    ptrs = (ctypes.c_void_p * calls)(*[copies[i % len(copies)].data_ptr() for i in range(calls)])
+    out = torch.empty(rows * 4 * 16, dtype=torch.int32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    nbytes = 2 * rows * row_len
+    print(f"single-pass read of {rows} x {row_len} fp16 ({nbytes} bytes), {calls} back-to-back "
+          f"launches over {len(copies)} input copies")
+    lib.read_floor_empty_run.restype = i32
+    lib.read_floor_empty_run.argtypes = [i32, i32, vp, vp]
+    lib.read_floor_empty_run(calls, rows, out.data_ptr(), stream.cuda_stream)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    lib.read_floor_empty_run(calls, rows, out.data_ptr(), stream.cuda_stream)
+    b.record(stream)
+    torch.cuda.synchronize()
+    print(f"empty kernel, {rows} workgroups x 1024 threads: {a.elapsed_time(b) * 1e3 / calls:.2f} us per launch")
+    print("workgroups per row | threads x vectors | us per launch | GB/s | fraction of 8 TB/s")
+    for block, vpt, w in FLOOR_SHAPES:
+        def go():
+            rc = lib.read_floor_run(ptrs, calls, rows, row_len, block, vpt, w, out.data_ptr(),
+                                    stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"read_floor_run returned {rc}")
+        go()  # warm-up
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        go()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / calls
+        print(f"{w} | {block} x {vpt} | {us:.2f} | {nbytes / us / 1e3:.0f} | {nbytes / us / 1e3 / 8000:.3f}")
+
+
+MATRIX = (
+    ("llm_logits", ["--k", "50"]),
+    ("uniform_small", ["--k", "50"]),
+    ("varlen", ["--k", "64"]),
+    ("ties_special", ["--k", "1"]),
+    ("ties_special", ["--k", "16"]),
+    ("ties_special", ["--k", "128"]),
+    ("ties_special", ["--k", "256"]),
+    ("huge_segment", ["--k", "1024"]),
+    ("llm_logits", ["--k", "50", "--dtype", "bf16"]),
+    ("llm_logits", ["--k", "50", "--op", "sample"]),
+) + tuple(("ref_matrix", ["--k", "50", "--seg-num", str(n), "--no-cpu-baseline"])
+          for n in (128, 1500, 3000, 4500, 6000))
+
+
+def run_matrix(out_path) -> None:
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    lines = ["| workload | options | us per step | segments/s | elements/s | roofline frac | "
+             "CPU 1 thread (segments/s) | CPU threaded | parity |", "|---|---|---|---|---|---|---|---|---|"]
+    for workload, opts in MATRIX:
+        cmd = [sys.executable, os.path.join(root, "bench.py"), "--workload", workload, *opts]
+        res = subprocess.run(cmd, capture_output=True, text=True, cwd=root)
+        if res.returncode != 0:
+            sys.stderr.write(res.stderr)
+            raise RuntimeError("bench.py failed: " + " ".join(cmd))
+        d = json.loads(res.stdout.strip().splitlines()[-1])
+        cpu = d.get("cpu_baseline") or {}
+        thr = cpu.get("threaded") or {}
+        row = (f"| {workload} | {' '.join(opts)} | {d['ms_per_step'] * 1e3:.2f} | {d['value']:.4g} | "
+               f"{d['elements_per_s']:.4g} | {d['roofline']['frac']:.3f} | "
+               f"{cpu.get('value', float('nan')):.4g} | "
+               f"{thr.get('value', float('nan')):.4g} ({thr.get('cores', '-')} cores) | "
+               f"{d['parity_spot_check']} |")
+        print(row, flush=True)
+        lines.append(row)
+    if out_path:
+        with open(out_path, "w") as f:
+            f.write("\n".join(lines) + "\n")
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -82,7 +185,18 @@ def main(argv=None) -> int:
     t.add_argument("--copy-write", required=True)
     t.add_argument("--copy-mib", type=int, default=256)
     t.add_argument("--out", default=None)
+    fl = sub.add_parser("floor")
+    fl.add_argument("--calls", type=int, default=2000)
+    mx = sub.add_parser("matrix")
+    mx.add_argument("--out", default=None)
     a = ap.parse_args(argv)
+
+    if a.cmd == "floor":
+        run_floor(a.calls)
+        return 0
+    if a.cmd == "matrix":
+        run_matrix(a.out)
+        return 0
 
     if a.cmd == "copy":
         run_copy(a.mib, a.reps)
