@@ -24,18 +24,22 @@ constexpr int kMaxChunk = 1024 * 16 * 8;
 //   arrive  u64 [kGroupBarriers][W]   per-barrier arrival slots (a slot holding this call's
 //                                     epoch has arrived)
 //   counts  u64 [2][W]                epoch-tagged list lengths (tag44 << 20 | length)
-//   hist    u32 [2][kGroupCopies][256] threshold histograms, each spread over kGroupCopies
-//                                     copies so that few workgroups add to one address
+//   hist    u32 [kGroupCopies][256]   threshold histogram of the thread bests' high key byte,
+//                                     spread over kGroupCopies copies so that few workgroups
+//                                     add to one address
+//   fine    u32 [kFineCopies][2048]   the same thread bests at 32-key resolution (key >> 5)
 //   rhist   u32 [6][256]              refinement digit histograms
 //   lists   u64 [W][kCandArea]        every workgroup's candidate list
 constexpr int kGroupBarriers = 10;
 constexpr int kGroupCopies = 16;
+constexpr int kFineCopies = 8;
+constexpr int kFineBins = 2048;
 // Longest whole-segment list the final ranking takes: it is gathered into the LDS from the
 // candidate area onward (area, selection, rank and staging regions, free by then), which
 // holds at least 6464 entries for every k.
 constexpr int kGroupCap = 6144;
 struct GroupLayout {
-  size_t flag, arrive, counts, hist, rhist, lists, bytes;
+  size_t flag, arrive, counts, hist, fine, rhist, lists, bytes;
 };
 constexpr size_t group_align(size_t x) { return (x + 127) / 128 * 128; }
 constexpr GroupLayout group_layout(int W) {
@@ -48,7 +52,9 @@ constexpr GroupLayout group_layout(int W) {
   L.counts = off;
   off += group_align(static_cast<size_t>(2) * W * 8);
   L.hist = off;
-  off += static_cast<size_t>(2) * kGroupCopies * 256 * 4;
+  off += static_cast<size_t>(kGroupCopies) * 256 * 4;
+  L.fine = off;
+  off += static_cast<size_t>(kFineCopies) * kFineBins * 4;
   L.rhist = off;
   off += static_cast<size_t>(6) * 256 * 4;
   L.lists = off;

@@ -482,7 +482,8 @@ struct GroupWs {
   u64* flag;    // epoch-tagged "histograms cleared"
   u64* arrive;  // [kGroupBarriers][W] arrival slots
   u64* counts;  // [2][W] epoch-tagged list lengths
-  u32* hist;    // [2][kGroupCopies][256]
+  u32* hist;    // [kGroupCopies][256]
+  u32* fine;    // [kFineCopies][kFineBins]
   u32* rhist;   // [6][256]
   u64* lists;   // [W][kCandArea]
 };
@@ -495,6 +496,7 @@ __device__ __forceinline__ GroupWs group_ws(const TopkParams& p, int seg) {
   g.arrive = reinterpret_cast<u64*>(b + L.arrive);
   g.counts = reinterpret_cast<u64*>(b + L.counts);
   g.hist = reinterpret_cast<u32*>(b + L.hist);
+  g.fine = reinterpret_cast<u32*>(b + L.fine);
   g.rhist = reinterpret_cast<u32*>(b + L.rhist);
   g.lists = reinterpret_cast<u64*>(b + L.lists);
   return g;
@@ -764,7 +766,8 @@ segmented_topk_kernel(TopkParams p) {
   if constexpr (COOP) {
     g = group_ws(p, seg);
     if (w == 0) {
-      for (int i = tid; i < 2 * kGroupCopies * 256; i += BLOCK) store_agent(g.hist + i, 0u);
+      for (int i = tid; i < kGroupCopies * 256; i += BLOCK) store_agent(g.hist + i, 0u);
+      for (int i = tid; i < kFineCopies * kFineBins; i += BLOCK) store_agent(g.fine + i, 0u);
       for (int i = tid; i < 6 * 256; i += BLOCK) store_agent(g.rhist + i, 0u);
       wait_vector_memory();
       __syncthreads();
@@ -789,7 +792,13 @@ segmented_topk_kernel(TopkParams p) {
     }
   }
   for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
-  __syncthreads();  // histogram cleared (the loads stay in flight)
+  if constexpr (COOP) {
+    // the 32-key resolution histogram of the cooperative threshold, in the (still unused)
+    // candidate area
+    u32* fine = reinterpret_cast<u32*>(sm.area);
+    for (int i = tid; i < kFineBins; i += BLOCK) fine[i] = 0;
+  }
+  __syncthreads();  // histograms cleared (the loads stay in flight)
   TOPK_TRACE(12);
   // Positions outside [lo, hi) become the filler.  lo > 0 only in a segment's first chunk,
   // where it is below 8, so only vector 0 can start before lo; whether a vector index reaches
@@ -831,12 +840,20 @@ segmented_topk_kernel(TopkParams p) {
   TOPK_TRACE(1);
   TOPK_WTRACE(1);
 
-  // ---- 3. threshold T = kc-th smallest thread best, by two histogram passes
+  // ---- 3. threshold T.  A single workgroup: the kc-th smallest thread best, exactly, by two
+  // LDS histogram passes (high byte, then low byte inside the boundary bucket).  A cooperative
+  // segment: the thread bests' high-byte histogram and a 32-key resolution one (key >> 5) are
+  // summed over the segment's workgroups in one meeting; T is the last key of the fine bin
+  // holding the kk-th best, so at least kk real elements are at or below it, and at most that
+  // bin's other keys' worth of extra elements pass.
   atomicAdd(&sm.hist[best_key >> 8], 1u);
   if (tid < 256) sm.hist2[tid] = 0;
   if (tid == 0) sm.scal[4] = 0;  // candidate list counter
-  __syncthreads();
+  u32 T;
   if constexpr (COOP) {
+    u32* fine = reinterpret_cast<u32*>(sm.area);
+    atomicAdd(&fine[best_key >> 5], 1u);
+    __syncthreads();
     if (tid == 0) {  // the global histograms are cleared
       for (u32 spin = 0; spin < kGroupSpinLimit; ++spin) {
         if (tagged_value(load_agent(g.flag), tag) == 1u) break;
@@ -844,24 +861,51 @@ segmented_topk_kernel(TopkParams p) {
       }
     }
     __syncthreads();
+    // this workgroup's nonzero fine bins into its copy; the coarse ones go in group_histogram
+    for (int i = tid; i < kFineBins; i += BLOCK) {
+      const u32 c = fine[i];
+      if (c) {
+        __hip_atomic_fetch_add(g.fine + (w % kFineCopies) * kFineBins + i, c, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
     group_histogram<BLOCK>(sm.hist, g.hist, sm.stage, g.arrive, epoch, w, Ws);
     TOPK_TRACE(8);
-  }
-  if (wid == 0) wave_find_bucket(sm.hist, need, sm.scal + 8, lane);
-  __syncthreads();
-  TOPK_TRACE(2);
-  const u32 b1 = static_cast<u32>(sm.scal[8]);
-  if ((best_key >> 8) == b1) atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
-  __syncthreads();
-  if constexpr (COOP) {
-    // Whole segment: an exact second byte as well (a coarse bucket bound would save this round
-    // of cross-workgroup latency but quadruple the list the final ranking has to sort).
-    group_histogram<BLOCK>(sm.hist2, g.hist + kGroupCopies * 256, sm.stage, g.arrive + W, epoch, w, Ws);
+    if (wid == 0) wave_find_bucket(sm.hist, need, sm.scal + 8, lane);
+    __syncthreads();
+    TOPK_TRACE(2);
+    const u32 b1 = static_cast<u32>(sm.scal[8]);
+    // the 8 fine bins of bucket b1, summed over the copies (thread t: bin t & 7, copy t >> 3)
+    if (tid < 8 * kFineCopies) {
+      sm.stage[tid] = load_agent(g.fine + (tid >> 3) * kFineBins + b1 * 8 + (tid & 7));
+    }
+    __syncthreads();
+    if (wid == 0) {
+      u32 c = 0;
+      if (lane < 8) {
+#pragma unroll
+        for (int q = 0; q < kFineCopies; ++q) c += sm.stage[q * 8 + lane];
+      }
+      const u32 incl = wave_inclusive_scan(c);
+      const u32 rest = static_cast<u32>(need - sm.scal[9]);  // rank inside bucket b1
+      const u64 m = ballot(lane < 8 && incl >= rest);
+      if (lane == static_cast<int>(__builtin_ctzll(m))) sm.scal[12] = lane;
+    }
+    __syncthreads();
+    T = (((b1 << 3) | static_cast<u32>(sm.scal[12])) << 5) | 31u;
     TOPK_TRACE(9);
+  } else {
+    __syncthreads();
+    if (wid == 0) wave_find_bucket(sm.hist, need, sm.scal + 8, lane);
+    __syncthreads();
+    TOPK_TRACE(2);
+    const u32 b1 = static_cast<u32>(sm.scal[8]);
+    if ((best_key >> 8) == b1) atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
+    __syncthreads();
+    if (wid == 0) wave_find_bucket(sm.hist2, need - sm.scal[9], sm.scal + 12, lane);
+    __syncthreads();
+    T = (b1 << 8) | static_cast<u32>(sm.scal[12]);
   }
-  if (wid == 0) wave_find_bucket(sm.hist2, need - sm.scal[9], sm.scal + 12, lane);
-  __syncthreads();
-  const u32 T = (b1 << 8) | static_cast<u32>(sm.scal[12]);
   TOPK_TRACE(4);
   TOPK_WTRACE(0);
 
