@@ -28,9 +28,11 @@
 //   5. output          index and raw value bits of each selected candidate.
 //
 // Segments longer than one chunk are split over W workgroups.  While the W lists fit one LDS
-// merge, each workgroup publishes its list to the workspace and the last to arrive (an
-// epoch-tagged arrival counter, so the workspace needs no initialisation) merges them with
-// step 4.  Beyond that (long segments with large k) the W workgroups run cooperatively, all
+// merge, they meet once through the workspace, which needs no initialisation.  Two chunks:
+// the workgroup that takes the segment's ticket first (an exchange issued while its loads are
+// in flight) publishes its list with every word tagged for the call, and the other polls for
+// it and merges it with its own list in step 4.  Three or more: each workgroup publishes, and
+// the last to arrive (an epoch-tagged arrival counter) merges.  Beyond that (long segments with large k) the W workgroups run cooperatively, all
 // co-resident: the threshold histograms of step 2 are summed over the whole segment in global
 // memory, each workgroup filters its chunk against the one segment threshold, and every
 // workgroup gathers the segment's candidate list and ranks a share of it.  Workgroups meet at
@@ -464,6 +466,24 @@ __device__ __forceinline__ bool arrive_last(u64* ticket, u64 epoch, int arrivals
   }
 }
 
+// Two-chunk segments.  Each workgroup swaps its mark (call epoch, chunk) into the segment's
+// ticket; the one that gets the other chunk's mark back arrived second and merges, and it
+// resets the ticket to zero.  A ticket left by any other call (or by the counter above, whose
+// low 16 bits are zero after each call) never equals a mark of this one.
+__device__ __forceinline__ u64 pair_mark(u64 epoch, int w) {
+  return (epoch << 2) | static_cast<u64>(w + 1);
+}
+// Published entries carry a tag in bits 18..31 of their index field (two-chunk segments have
+// indices below 2^18) with the top bit set, which no plain index has; the length word carries
+// a 16-bit tag with the top bit set above the length.
+constexpr u64 kPairTagMask = 0x3fffull << 34;
+__device__ __forceinline__ u64 pair_entry_tag(u64 epoch) {
+  return (0x2000ull | (epoch & 0x1fffu)) << 34;
+}
+__device__ __forceinline__ u32 pair_count_tag(u64 epoch) {
+  return 0x8000u | static_cast<u32>(epoch & 0x7fffu);
+}
+
 // Orders a wave's LDS writes before its lanes read each other's entries (and the reads before
 // the next overwrite): LDS requests of one wave are served in order, so this only has to keep
 // the compiler from moving them across.
@@ -698,7 +718,8 @@ __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
 segmented_topk_kernel(TopkParams p) {
   constexpr int NW = BLOCK / 64;
   constexpr int CH = BLOCK * VPT * 8;
-  static_assert(CH <= 65536 * 2, "chunk positions must fit the refinement packing");
+  static_assert(CH <= 65536 * 2, "chunk positions must fit the refinement packing, and the "
+                                 "indices of a two-chunk segment 18 bits");
   static_assert(NW <= 16, "at most 16 waves");
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const Smem sm = carve_smem(smem_raw, p.kpad);
@@ -748,6 +769,8 @@ segmented_topk_kernel(TopkParams p) {
   if (w >= Ws) return;
 
   const int kk = n < k ? static_cast<int>(n) : k;
+  // A two-chunk segment merges through one published list (step 5).
+  const bool pair = !COOP && BLOCK >= 512 && Ws == 2 && p.cap_list <= BLOCK;
   const int64_t cb = a0 + static_cast<int64_t>(w) * CH;
   const int64_t c0 = s0 > cb ? s0 : cb;
   const int64_t c1 = s1 < cb + CH ? s1 : cb + CH;
@@ -790,6 +813,15 @@ segmented_topk_kernel(TopkParams p) {
       const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, tid * 16, j * BLOCK * 16, kCachePolicyNT);
       v[j] = make_uint4(t.x, t.y, t.z, t.w);
     }
+  }
+  // Two-chunk segment: its arrival ticket is taken now, while the loads are in flight.  The
+  // workgroup that finds the other's mark arrived second and merges (step 5), gathering one
+  // published entry per thread (cap_list <= BLOCK).  Both workgroups see the same parameters,
+  // so both take this path or neither does.
+  u64 pair_seen = 0;
+  if (pair && tid == 0) {
+    pair_seen = __hip_atomic_exchange(p.tickets + seg, pair_mark(epoch, w), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
   }
   for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
   if constexpr (COOP) {
@@ -1038,6 +1070,10 @@ segmented_topk_kernel(TopkParams p) {
     }
   }
   TOPK_TRACE(5);
+  if (pair && tid == 0) {
+    sm.scal[5] = pair_seen == pair_mark(epoch, 1 - w) ? 1 : 0;
+    sm.scal[6] = 0;  // stale-word reports of the merger's poll
+  }
   __syncthreads();
   TOPK_WTRACE(5);
 
@@ -1203,60 +1239,120 @@ segmented_topk_kernel(TopkParams p) {
   TOPK_TRACE_VALUE(14, C);
   TOPK_TRACE_VALUE(15, T);
 
-  // ---- 5. single-chunk segment: select and write
-  if (Ws == 1) {
-    finalize_segment<BLOCK>(p, sm, C, kk, n, seg);
-    TOPK_TRACE(7);
-    return;
-  }
-
-  // ---- 6. multi-chunk segment: publish this chunk's list, last arriver merges
-  const u64* src = sm.area;
-  int M = C;
-  if (C > p.cap_list) {
-    const u64 bound = block_select_bound<BLOCK>(sm.area, C, kc, sm.hist, sm.scal);
-    if (tid == 0) sm.scal[3] = 0;
-    __syncthreads();
-    for (int i = tid; i < C; i += BLOCK) {
-      const u64 P = sm.area[i];
-      if (P <= bound) {
-        const int slot = atomicAdd(&sm.scal[3], 1);
-        if (slot < p.kpad) sm.sel[slot] = P;
+  // ---- 5. multi-chunk segment: publish this chunk's list; the workgroup that merges goes
+  // on to step 6 with the segment's lists gathered in LDS.
+  int Mf = C;  // entries in sm.area that step 6 selects from
+  if (Ws > 1) {
+    const u64* src = sm.area;
+    int M = C;
+    if (C > p.cap_list) {
+      const u64 bound = block_select_bound<BLOCK>(sm.area, C, kc, sm.hist, sm.scal);
+      if (tid == 0) sm.scal[3] = 0;
+      __syncthreads();
+      for (int i = tid; i < C; i += BLOCK) {
+        const u64 P = sm.area[i];
+        if (P <= bound) {
+          const int slot = atomicAdd(&sm.scal[3], 1);
+          if (slot < p.kpad) sm.sel[slot] = P;
+        }
       }
+      __syncthreads();
+      src = sm.sel;
+      M = kc;
+    }
+    if (pair) {
+      // Two chunks.  The first to arrive publishes its list (at most cap_list entries holding
+      // its chunk's top kc) with every entry and the length word tagged for this call, and
+      // returns without waiting for the stores.  The second gathers it into LDS after its
+      // own list, polling until the length and every entry carry the tag, then clears the
+      // consumed words (so a replay with the same epoch cannot take them for fresh ones) and
+      // the ticket.
+      const u64 etag = pair_entry_tag(epoch);
+      const u32 ctag = pair_count_tag(epoch);
+      if (!sm.scal[5]) {
+        const int64_t my_id = static_cast<int64_t>(seg) * W + w;
+        u64* dst = p.lists + my_id * p.cap_list;
+        for (int i = tid; i < M; i += BLOCK) store_agent(dst + i, src[i] | etag);
+        if (tid == 0) {
+          store_agent(reinterpret_cast<u32*>(p.list_counts) + my_id, (ctag << 16) | static_cast<u32>(M));
+        }
+        TOPK_TRACE(8);
+        return;
+      }
+      if (src != sm.area) {
+        for (int i = tid; i < M; i += BLOCK) sm.area[i] = src[i];
+      }
+      const int64_t other = static_cast<int64_t>(seg) * W + (1 - w);
+      u64* ol = p.lists + other * p.cap_list;
+      u32* oc = reinterpret_cast<u32*>(p.list_counts) + other;
+      const int cap = p.cap_list;
+      int mp = 0;
+      int seen = 0;  // workgroup-uniform count of waves that found a stale word so far
+      u32 spin = 0;
+      for (;; ++spin) {
+        const u32 h = load_agent(oc);
+        const u64 x = tid < cap ? load_agent(ol + tid) : 0ull;
+        mp = static_cast<int>(h & 0xffffu);
+        mp = mp < cap ? mp : cap;
+        const bool bad = (h >> 16) != ctag || (tid < mp && (x & kPairTagMask) != etag);
+        if (ballot(bad) && lane == 0) atomicAdd(&sm.scal[6], 1);
+        __syncthreads();
+        const int now = sm.scal[6];
+        if (now == seen) {  // no wave saw a stale word: the list is complete
+          if (tid < mp) sm.area[M + tid] = x & ~kPairTagMask;
+          break;
+        }
+        seen = now;
+        if (spin >= kGroupSpinLimit) {  // the publisher never arrived: cannot happen
+          mp = 0;
+          break;
+        }
+        __syncthreads();  // every wave has read the count before the next round adds to it
+        __builtin_amdgcn_s_sleep(1);
+      }
+      TOPK_TRACE_VALUE(13, spin + 1);
+      if (tid < mp) store_agent(ol + tid, 0ull);
+      if (tid == 0) {
+        store_agent(oc, 0u);
+        store_agent(p.tickets + seg, 0ull);
+      }
+      Mf = M + mp;
+    } else {
+      // Three or more chunks: every workgroup publishes, the last to arrive merges.
+      const int64_t list_id = static_cast<int64_t>(seg) * W + w;
+      u64* my_list = p.lists + list_id * p.cap_list;
+      for (int i = tid; i < M; i += BLOCK) {
+        __hip_atomic_store(my_list + i, src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (tid == 0) __hip_atomic_store(p.list_counts + list_id, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wait_vector_memory();
+      __syncthreads();
+      TOPK_TRACE(8);
+      if (tid == 0) sm.scal[5] = arrive_last(p.tickets + seg, p.epoch, Ws) ? 1 : 0;
+      __syncthreads();
+      TOPK_TRACE(9);
+      if (!sm.scal[5]) return;
+
+      int total = 0;
+      for (int c = 0; c < Ws; ++c) {
+        const int64_t id = static_cast<int64_t>(seg) * W + c;
+        int cnt = __hip_atomic_load(p.list_counts + id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        cnt = cnt < 0 ? 0 : (cnt > p.cap_list ? p.cap_list : cnt);
+        if (total + cnt > kArea) cnt = kArea - total;
+        const u64* lst = p.lists + id * p.cap_list;
+        for (int i = tid; i < cnt; i += BLOCK) {
+          sm.area[total + i] = __hip_atomic_load(lst + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        total += cnt;
+      }
+      Mf = total;
     }
     __syncthreads();
-    src = sm.sel;
-    M = kc;
+    TOPK_TRACE(10);
   }
-  const int64_t list_id = static_cast<int64_t>(seg) * W + w;
-  u64* my_list = p.lists + list_id * p.cap_list;
-  for (int i = tid; i < M; i += BLOCK) {
-    __hip_atomic_store(my_list + i, src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (tid == 0) __hip_atomic_store(p.list_counts + list_id, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  wait_vector_memory();
-  __syncthreads();
-  TOPK_TRACE(8);
-  if (tid == 0) sm.scal[5] = arrive_last(p.tickets + seg, p.epoch, Ws) ? 1 : 0;
-  __syncthreads();
-  TOPK_TRACE(9);
-  if (!sm.scal[5]) return;
 
-  int total = 0;
-  for (int c = 0; c < Ws; ++c) {
-    const int64_t id = static_cast<int64_t>(seg) * W + c;
-    int cnt = __hip_atomic_load(p.list_counts + id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    cnt = cnt < 0 ? 0 : (cnt > p.cap_list ? p.cap_list : cnt);
-    if (total + cnt > kArea) cnt = kArea - total;
-    const u64* lst = p.lists + id * p.cap_list;
-    for (int i = tid; i < cnt; i += BLOCK) {
-      sm.area[total + i] = __hip_atomic_load(lst + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    total += cnt;
-  }
-  __syncthreads();
-  TOPK_TRACE(10);
-  finalize_segment<BLOCK>(p, sm, total, kk, n, seg);
+  // ---- 6. select and write the segment's row
+  finalize_segment<BLOCK>(p, sm, Mf, kk, n, seg);
   TOPK_TRACE(11);
 }
 
