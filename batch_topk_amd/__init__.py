@@ -40,7 +40,15 @@ EXPORTED_SYMBOLS = (
     "radix_topk_sample_half_workspace_size",
     "radix_topk_sample_bf16",
     "radix_topk_sample_bf16_workspace_size",
+    "radix_topk_batch_topk_ex",
+    "radix_topk_batch_topk_ex_workspace_size",
 )
+
+# radix_topk_batch_topk_ex element formats and output flags (include/batch_topk.h)
+FORMAT_F16 = 0
+FORMAT_BF16 = 1
+UNSORTED = 1
+INDICES_ONLY = 2
 
 _lib = None
 
@@ -86,6 +94,10 @@ def load_library():
             ws = getattr(L, name + "_workspace_size")
             ws.restype = sz
             ws.argtypes = [i32, i32, i32]
+        L.radix_topk_batch_topk_ex.restype = i32
+        L.radix_topk_batch_topk_ex.argtypes = [vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, sz, vp]
+        L.radix_topk_batch_topk_ex_workspace_size.restype = sz
+        L.radix_topk_batch_topk_ex_workspace_size.argtypes = [i32, i32, i32, i32, i32]
         _lib = L
     return _lib
 
@@ -174,6 +186,21 @@ def sample_bf16_workspace_size(seg_num: int, seg_len: int, k: int) -> int:
     return int(load_library().radix_topk_sample_bf16_workspace_size(seg_num, seg_len, k))
 
 
+def batch_topk_ex(d_input: int, fmt: int, d_offsets: int, seg_num: int, seg_len: int, k: int,
+                  flags: int, d_output_values: int, d_output_indices: int, d_workspace: int,
+                  workspace_bytes: int, stream: int = 0) -> int:
+    """radix_topk_batch_topk_ex (include/batch_topk.h): any layout (d_offsets 0 = fixed
+    length), format (FORMAT_F16 / FORMAT_BF16) and output flags (UNSORTED, INDICES_ONLY)."""
+    return int(load_library().radix_topk_batch_topk_ex(
+        d_input, fmt, d_offsets or None, seg_num, seg_len, k, flags, d_output_values or None,
+        d_output_indices, d_workspace, workspace_bytes, stream))
+
+
+def batch_topk_ex_workspace_size(fmt: int, segmented: bool, seg_num: int, seg_len: int, k: int) -> int:
+    return int(load_library().radix_topk_batch_topk_ex_workspace_size(fmt, int(bool(segmented)),
+                                                                      seg_num, seg_len, k))
+
+
 # ------------------------------------------------------------------ torch conveniences
 
 def _entry_points(dtype):
@@ -195,16 +222,49 @@ def _stream_handle(stream) -> int:
     return int(s.cuda_stream)
 
 
-def topk(x, k: int, workspace=None, stream=None):
+def _format_of(dtype) -> int:
+    import torch
+
+    if dtype == torch.float16:
+        return FORMAT_F16
+    if dtype == torch.bfloat16:
+        return FORMAT_BF16
+    raise ValueError(f"unsupported dtype {dtype}: float16 or bfloat16")
+
+
+def _topk_ex(x, offsets, seg_num, seg_len, k, sorted, values, workspace, stream):
+    import torch
+
+    fmt = _format_of(x.dtype)
+    flags = (0 if sorted else UNSORTED) | (0 if values else INDICES_ONLY)
+    ws_bytes = batch_topk_ex_workspace_size(fmt, offsets is not None, seg_num, seg_len, k)
+    if ws_bytes == 0:
+        raise TopkError(HIP_ERROR_INVALID_VALUE, "radix_topk_batch_topk_ex_workspace_size")
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    vals = torch.empty((seg_num, k), dtype=x.dtype, device=x.device) if values else None
+    idx = torch.empty((seg_num, k), dtype=torch.int32, device=x.device)
+    rc = batch_topk_ex(x.data_ptr(), fmt, offsets.data_ptr() if offsets is not None else 0, seg_num,
+                       seg_len, k, flags, vals.data_ptr() if values else 0, idx.data_ptr(),
+                       workspace.data_ptr(), workspace.numel(), _stream_handle(stream))
+    if rc != HIP_SUCCESS:
+        raise TopkError(rc, "radix_topk_batch_topk_ex")
+    return vals, idx
+
+
+def topk(x, k: int, workspace=None, stream=None, sorted: bool = True, values: bool = True):
     """Top-k of every row of a contiguous float16 or bfloat16 CUDA tensor [seg_num, seg_len].
 
     Returns (values [seg_num, k] of x's dtype, indices int32 [seg_num, k]).  ``workspace``
-    may be a uint8 CUDA tensor of at least the workspace size of the shape.
+    may be a uint8 CUDA tensor of at least the workspace size of the shape.  ``sorted=False``
+    returns each row's top-k in unspecified order; ``values=False`` returns (None, indices).
     """
     import torch
 
     if x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
         raise ValueError("topk expects a contiguous 2-D float16 or bfloat16 CUDA tensor")
+    if not (sorted and values):
+        return _topk_ex(x, None, x.shape[0], x.shape[1], k, sorted, values, workspace, stream)
     fixed, fixed_ws, _, _ = _entry_points(x.dtype)
     seg_num, seg_len = x.shape
     ws_bytes = fixed_ws(seg_num, seg_len, k)
@@ -221,12 +281,13 @@ def topk(x, k: int, workspace=None, stream=None):
     return vals, idx
 
 
-def segmented_topk(x, offsets, k: int, max_seg_len: int, workspace=None, stream=None):
+def segmented_topk(x, offsets, k: int, max_seg_len: int, workspace=None, stream=None,
+                   sorted: bool = True, values: bool = True):
     """Top-k of every segment x[offsets[s]:offsets[s+1]] of a 1-D float16 or bfloat16 CUDA
     tensor.
 
     ``offsets`` is an int32 CUDA tensor of seg_num + 1 entries.  Ranks beyond a segment's
-    length hold index -1 and value bits 0xFFFF.
+    length hold index -1 and value bits 0xFFFF.  ``sorted`` and ``values`` as for topk.
     """
     import torch
 
@@ -234,6 +295,9 @@ def segmented_topk(x, offsets, k: int, max_seg_len: int, workspace=None, stream=
         raise ValueError("segmented_topk expects a contiguous float16 or bfloat16 CUDA tensor")
     if offsets.dtype != torch.int32 or not offsets.is_cuda or offsets.dim() != 1:
         raise ValueError("offsets must be a 1-D int32 CUDA tensor")
+    if not (sorted and values):
+        return _topk_ex(x, offsets, offsets.numel() - 1, max_seg_len, k, sorted, values,
+                        workspace, stream)
     _, _, seg, seg_ws = _entry_points(x.dtype)
     seg_num = offsets.numel() - 1
     ws_bytes = seg_ws(seg_num, max_seg_len, k)

@@ -146,7 +146,8 @@ struct SampleSpec {
 
 int run(const Plan& plan, uint32_t inf_bits, const uint16_t* d_input, const int32_t* d_offsets,
         int seg_num, int64_t seg_len, int64_t max_len, int k, uint16_t* d_values, int32_t* d_indices,
-        void* d_workspace, size_t workspace_bytes, void* stream, const SampleSpec* sample = nullptr) {
+        void* d_workspace, size_t workspace_bytes, void* stream, const SampleSpec* sample = nullptr,
+        bool unsorted = false) {
   if (!plan.ok || workspace_bytes < plan.ws_bytes) return kInvalid;
   const uintptr_t in_addr = reinterpret_cast<uintptr_t>(d_input);
   if ((in_addr & 1u) || (reinterpret_cast<uintptr_t>(d_values) & 1u) ||
@@ -166,7 +167,8 @@ int run(const Plan& plan, uint32_t inf_bits, const uint16_t* d_input, const int3
   p.cap_list = plan.cap_list;
   p.cand_area = plan.cand_area;
   p.kpad = plan.kpad;
-  p.out_vals = d_values;
+  p.out_vals = d_values;  // nullptr: indices only
+  p.unsorted = unsorted ? 1 : 0;
   p.out_idx = d_indices;
   const uintptr_t ws = align_up(reinterpret_cast<uintptr_t>(d_workspace), kAlign);
   size_t off = 0;
@@ -235,6 +237,33 @@ int segmented_topk(uint32_t inf_bits, const uint16_t* d_input, const int32_t* d_
   const Plan plan = make_plan(seg_num, max_seg_len, k);
   return run(plan, inf_bits, d_input, d_offsets, seg_num, 0, max_seg_len, k, d_output_values,
              d_output_indices, d_workspace, workspace_bytes, stream);
+}
+
+// Extended entry point: element format, fixed-length or segmented input, output flags.
+bool known_format(int format) {
+  return format == RADIX_TOPK_FORMAT_F16 || format == RADIX_TOPK_FORMAT_BF16;
+}
+
+size_t ex_workspace_size(int format, int segmented, int seg_num, int seg_len, int k) {
+  if (!known_format(format)) return 0;
+  return segmented ? segmented_workspace_size(seg_num, seg_len, k) : fixed_workspace_size(seg_num, seg_len, k);
+}
+
+int topk_ex(const void* d_input, int format, const int32_t* d_offsets, int seg_num, int seg_len, int k,
+            int flags, void* d_output_values, int32_t* d_output_indices, void* d_workspace,
+            size_t workspace_bytes, void* stream) {
+  if (!known_format(format)) return kInvalid;
+  if (flags & ~(RADIX_TOPK_UNSORTED | RADIX_TOPK_INDICES_ONLY)) return kInvalid;
+  const bool indices_only = (flags & RADIX_TOPK_INDICES_ONLY) != 0;
+  if (seg_num <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return kInvalid;
+  if (d_offsets ? seg_len < 0 : (seg_len <= 0 || k > seg_len)) return kInvalid;
+  if (!d_input || !d_output_indices || !d_workspace || (!indices_only && !d_output_values)) return kInvalid;
+  const Plan plan = make_plan(seg_num, seg_len, k);
+  const uint32_t inf = format == RADIX_TOPK_FORMAT_BF16 ? kInfBitsBF16 : kInfBitsF16;
+  uint16_t* vals = indices_only ? nullptr : static_cast<uint16_t*>(d_output_values);
+  return run(plan, inf, static_cast<const uint16_t*>(d_input), d_offsets, seg_num, d_offsets ? 0 : seg_len,
+             seg_len, k, vals, d_output_indices, d_workspace, workspace_bytes, stream, nullptr,
+             (flags & RADIX_TOPK_UNSORTED) != 0);
 }
 
 // Top-k of every row, then one draw per row from the softmax of its top-k.
@@ -310,6 +339,19 @@ int radix_topk_batch_topk_bf16_segmented(const uint16_t* d_input, const int32_t*
   return radix_topk_amd::segmented_topk(kInfBitsBF16, d_input, d_offsets, seg_num, max_seg_len, k,
                                         d_output_values, d_output_indices, d_workspace,
                                         workspace_bytes, stream);
+}
+
+size_t radix_topk_batch_topk_ex_workspace_size(int format, int segmented, int seg_num, int seg_len,
+                                               int k) {
+  return radix_topk_amd::ex_workspace_size(format, segmented, seg_num, seg_len, k);
+}
+
+int radix_topk_batch_topk_ex(const void* d_input, int format, const int32_t* d_offsets, int seg_num,
+                             int seg_len, int k, int flags, void* d_output_values,
+                             int32_t* d_output_indices, void* d_workspace, size_t workspace_bytes,
+                             void* stream) {
+  return radix_topk_amd::topk_ex(d_input, format, d_offsets, seg_num, seg_len, k, flags, d_output_values,
+                                 d_output_indices, d_workspace, workspace_bytes, stream);
 }
 
 size_t radix_topk_sample_half_workspace_size(int seg_num, int seg_len, int k) {

@@ -88,7 +88,8 @@ struct TopkParams {
   int32_t cand_area;            // LDS entries of the candidate / merge area
   int32_t kpad;                 // LDS entries of the selection area (power of two >= k)
   int32_t cooperative;          // 1: whole-segment threshold across the segment's workgroups
-  uint16_t* out_vals;           // [seg_num, k]
+  uint16_t* out_vals;           // [seg_num, k], or nullptr: indices only
+  int32_t unsorted;             // 1: each row's selected set in unspecified order
   int32_t* out_idx;             // [seg_num, k]
   unsigned long long* tickets;  // [seg_num] arrival words (epoch << 16 | count)
   int32_t* list_counts;         // [seg_num * W]

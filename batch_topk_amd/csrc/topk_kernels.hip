@@ -256,6 +256,13 @@ __device__ u64 block_select_bound(const u64* list, int M, int kk, u32* hist, int
   return prefix | ~pmask;
 }
 
+// Writes the pad (index -1, value bits 0xFFFF) at output slot o; indices-only calls have no
+// value array.
+__device__ __forceinline__ void write_pad(const TopkParams& p, int64_t o) {
+  p.out_idx[o] = -1;
+  if (p.out_vals) p.out_vals[o] = 0xffffu;
+}
+
 // Writes rank r of the segment's output row.  An entry outside the segment (only a padding
 // sentinel can be) is written as the pad.
 __device__ __forceinline__ void write_rank(const TopkParams& p, int64_t n, int seg, int r, u64 P) {
@@ -264,10 +271,9 @@ __device__ __forceinline__ void write_rank(const TopkParams& p, int64_t n, int s
   if (r >= p.k) return;
   if (static_cast<int64_t>(idx) < n) {
     p.out_idx[o] = static_cast<int>(idx);
-    p.out_vals[o] = static_cast<uint16_t>(cand_raw(P));
+    if (p.out_vals) p.out_vals[o] = static_cast<uint16_t>(cand_raw(P));
   } else {
-    p.out_idx[o] = -1;
-    p.out_vals[o] = 0xffffu;
+    write_pad(p, o);
   }
 }
 
@@ -391,6 +397,8 @@ __device__ __forceinline__ void sample_segment(const TopkParams& p, const u64* s
 
 // Select the kk best of the M packed candidates in `sm.area` (M >= kk) and write them, in
 // order, to the segment's output row; ranks kk..k-1 get the pad (index -1, bits 0xFFFF).
+// An unsorted call writes the same kk entries to slots 0..kk-1 in unspecified order when the
+// list is longer than 128 (shorter lists are ranked anyway: the ranking is the selection).
 // With top-k sampling on, the ranked entries are also kept in LDS (sm.sel, or sm.area when
 // sm.sel holds the selection) and wave 0 then draws the segment's sample.
 template <int BLOCK>
@@ -400,17 +408,30 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
   if (M < kk) kk = M;  // cannot happen (every candidate list holds >= kk entries); keeps it safe
   for (int r = kk + tid; r < p.k; r += BLOCK) {
     const int64_t o = static_cast<int64_t>(seg) * p.k + r;
-    p.out_idx[o] = -1;
-    p.out_vals[o] = 0xffffu;
+    write_pad(p, o);
   }
   const bool sampling = p.samples != nullptr;
   constexpr int NW = BLOCK / 64;
   u64* sorted = sm.sel;
-  // Small sets: one DPP row per candidate counts the smaller entries (row_rank_write); up to
-  // 512: every wave ranks its share against the whole list held in registers.
+  // Small sets: one DPP row per candidate counts the smaller entries (row_rank_write).
   if (M <= 128) {
     row_rank_write<BLOCK>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+  } else if (p.unsorted && !sampling) {
+    // Unsorted output: the kk best, found by radix select, in the order they are found.
+    if (M > kk) {
+      const u64 bound = block_select_bound<BLOCK>(sm.area, M, kk, sm.hist, sm.scal);
+      if (tid == 0) sm.scal[3] = 0;
+      __syncthreads();
+      for (int i = tid; i < M; i += BLOCK) {
+        const u64 P = sm.area[i];
+        if (P <= bound) write_rank(p, n, seg, atomicAdd(&sm.scal[3], 1), P);
+      }
+    } else {
+      for (int i = tid; i < M; i += BLOCK) write_rank(p, n, seg, i, sm.area[i]);
+    }
   } else if (NW >= 8 && M <= 8 * NW * 4 && M <= 512) {
+    // Up to 512: every wave ranks its share against the whole list held in registers (a
+    // radix select first costs more: tied keys take it through the index digits).
     if constexpr (NW >= 8) wave_rank_write<BLOCK, 8>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
   } else {
     const u64* sel = sm.area;
@@ -758,8 +779,7 @@ segmented_topk_kernel(TopkParams p) {
     if (w == 0) {
       for (int r = tid; r < k; r += BLOCK) {
         const int64_t o = static_cast<int64_t>(seg) * k + r;
-        p.out_idx[o] = -1;
-        p.out_vals[o] = 0xffffu;
+        write_pad(p, o);
       }
       if (!COOP && p.samples) sample_segment(p, nullptr, 0, seg);
     }
@@ -1168,8 +1188,7 @@ segmented_topk_kernel(TopkParams p) {
     if (w == 0) {
       for (int r = kk + tid; r < k; r += BLOCK) {
         const int64_t o = static_cast<int64_t>(seg) * k + r;
-        p.out_idx[o] = -1;
-        p.out_vals[o] = 0xffffu;
+        write_pad(p, o);
       }
     }
     const int per = (static_cast<int>(total) + Ws - 1) / Ws;

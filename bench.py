@@ -20,9 +20,12 @@ ref_matrix --seg-num N for the reference's own benchmark matrix) print the same 
 that configuration.  --dtype bf16 runs the bfloat16 entry points on the same workload
 rounded to bfloat16 (no CPU baseline: that is the reference's fp16 verifier).  --op sample
 times the top-k sampling consumer (radix_topk_sample_*: the top-k, then one draw per row
-from the softmax of its top-k at --temperature) on fixed-length workloads.
+from the softmax of its top-k at --temperature) on fixed-length workloads.  --output times an
+output variant of radix_topk_batch_topk_ex (unsorted rows, indices only, or both); its
+algorithmic bytes count 4 bytes per output rank when no values are written.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--k K] [--dtype f16|bf16]
+                       [--op topk|sample] [--output sorted|unsorted|indices|unsorted-indices]
 """
 
 from __future__ import annotations
@@ -129,6 +132,8 @@ def main() -> int:
     ap.add_argument("--dtype", choices=("f16", "bf16"), default="f16")
     ap.add_argument("--op", choices=("topk", "sample"), default="topk")
     ap.add_argument("--temperature", type=float, default=1.0)
+    ap.add_argument("--output", choices=("sorted", "unsorted", "indices", "unsorted-indices"),
+                    default="sorted", help="output variant of radix_topk_batch_topk_ex (top-k only)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the engine has no "
@@ -145,6 +150,11 @@ def main() -> int:
     k = args.k
     if args.op == "sample" and offsets_of(args.workload):
         raise SystemExit("--op sample runs on fixed-length workloads")
+    flags = {"sorted": 0, "unsorted": bt.UNSORTED, "indices": bt.INDICES_ONLY,
+             "unsorted-indices": bt.UNSORTED | bt.INDICES_ONLY}[args.output]
+    if flags and args.op == "sample":
+        raise SystemExit("--output applies to --op topk")
+    ex_format = bt.FORMAT_F16 if args.dtype == "f16" else bt.FORMAT_BF16
     if args.dtype == "bf16":
         # the same workload rounded to bfloat16 (round to nearest even)
         bits = torch.from_numpy(bits.view(np.float16).astype(np.float32)).bfloat16() \
@@ -186,6 +196,12 @@ def main() -> int:
             rc = sample_fn(inputs[i % copies].data_ptr(), seg_num, seg_len, k, args.temperature,
                            uniforms.data_ptr(), vals.data_ptr(), idx.data_ptr(), 0, samples.data_ptr(),
                            ws.data_ptr(), ws_bytes, sh)
+        elif flags:
+            rc = bt.batch_topk_ex(inputs[i % copies].data_ptr(), ex_format,
+                                  0 if offsets is None else d_off.data_ptr(), seg_num,
+                                  seg_len if offsets is None else cfg["max_seg_len"], k, flags,
+                                  0 if flags & bt.INDICES_ONLY else vals.data_ptr(), idx.data_ptr(),
+                                  ws.data_ptr(), ws_bytes, sh)
         elif offsets is None:
             rc = fixed(inputs[i % copies].data_ptr(), seg_num, seg_len, k, vals.data_ptr(),
                        idx.data_ptr(), ws.data_ptr(), ws_bytes, sh)
@@ -211,7 +227,12 @@ def main() -> int:
                                    fmt=args.dtype)
     gi = idx.cpu().numpy()[:8]
     gv = vals.cpu().numpy().view(np.uint16)[:8]
-    parity_ok = bool(np.array_equal(gi, ei) and np.array_equal(gv, ev))
+    if flags & bt.UNSORTED:
+        # the same (index, value) set per row, in any order (pads: index -1 sorts first)
+        go, eo = np.argsort(gi, axis=1, kind="stable"), np.argsort(ei, axis=1, kind="stable")
+        gi, ei = np.take_along_axis(gi, go, 1), np.take_along_axis(ei, eo, 1)
+        gv, ev = np.take_along_axis(gv, go, 1), np.take_along_axis(ev, eo, 1)
+    parity_ok = bool(np.array_equal(gi, ei) and (bool(flags & bt.INDICES_ONLY) or np.array_equal(gv, ev)))
     log(f"parity spot check (8 segments vs oracle): {'ok' if parity_ok else 'MISMATCH'}")
 
     # Timed region: K back-to-back steps, events on the launch stream.
@@ -244,7 +265,8 @@ def main() -> int:
 
     # Algorithmic bytes: every input element read once (2 B), every output rank written once
     # (2 B value + 4 B index), plus the offsets array when given.
-    alg_bytes = 2 * n_elements + 6 * seg_num * k + (0 if offsets is None else 4 * (seg_num + 1))
+    out_bytes = 4 if flags & bt.INDICES_ONLY else 6
+    alg_bytes = 2 * n_elements + out_bytes * seg_num * k + (0 if offsets is None else 4 * (seg_num + 1))
     if args.op == "sample":
         alg_bytes += 8 * seg_num  # one uniform in, one sampled index out per row
     # The kernel's average launch duration over the timed region (back-to-back launches,
@@ -253,9 +275,10 @@ def main() -> int:
     achieved = alg_bytes / (step_us * 1e-6)
     value = seg_num * steps / (total_ms * 1e-3)
     dname = "fp16" if args.dtype == "f16" else "bf16"
-    metric = METRIC if (args.workload == "llm_logits" and k == 50 and args.dtype == "f16" and args.op == "topk") else \
+    metric = METRIC if (args.workload == "llm_logits" and k == 50 and args.dtype == "f16" and args.op == "topk"
+                        and not flags) else \
         f"segments/s and achieved HBM GB/s, {dname} top-{k}{' sampling' if args.op == 'sample' else ''} " \
-        f"over {cfg['workload'].split(':')[0]}"
+        f"over {cfg['workload'].split(':')[0]}{'' if not flags else f' ({args.output} output)'}"
     result = {
         "metric": metric,
         "value": value,
@@ -270,6 +293,7 @@ def main() -> int:
         "dtype": "u16" if args.dtype == "f16" else "u16 (bf16 keys)",
         "data": "synthetic",
         "config": dict(cfg, k=k, input_copies=copies, parallelism="single GPU",
+                       **({"output": args.output} if flags else {}),
                        **({"op": "top-k sampling", "temperature": args.temperature} if args.op == "sample" else {})),
         "roofline": {
             "bound": "hbm",
@@ -278,7 +302,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_BPS,
             "traffic": load_traffic(args.workload if args.dtype == "f16" else f"{args.workload}:bf16", k)
-            if args.op == "topk" else None,
+            if args.op == "topk" and not flags else None,
         },
         "elements_per_s": n_elements * steps / (total_ms * 1e-3),
         "hbm_gbps_whole_job": alg_bytes * steps / (total_ms * 1e-3) / 1e9,
@@ -294,7 +318,7 @@ def main() -> int:
         target = REF_MATRIX_TARGET_US.get((seg_num, seg_len, k))
         result["reference_target_us_rtx4080"] = target
         result["target_over_measured"] = None if target is None else target / (ms_per_step * 1e3)
-    if not args.no_cpu_baseline and offsets is None and args.dtype == "f16" and args.op == "topk":
+    if not args.no_cpu_baseline and offsets is None and args.dtype == "f16" and args.op == "topk" and not flags:
         log("timing the CPU baseline (reference host verifier)...")
         t0 = time.time()
         result["cpu_baseline"] = cpu_baseline(bits, k, args.cpu_threads)

@@ -134,6 +134,40 @@ int radix_topk_sample_bf16(const uint16_t* d_logits, int seg_num, int seg_len, i
                            void* d_workspace, size_t workspace_bytes, void* stream);
 size_t radix_topk_sample_bf16_workspace_size(int seg_num, int seg_len, int k);
 
+/* Element formats and output flags of radix_topk_batch_topk_ex. */
+#define RADIX_TOPK_FORMAT_F16 0  /* IEEE binary16 bit patterns */
+#define RADIX_TOPK_FORMAT_BF16 1 /* bfloat16 bit patterns */
+#define RADIX_TOPK_UNSORTED 1     /* each row's selected entries in unspecified order */
+#define RADIX_TOPK_INDICES_ONLY 2 /* no values: d_output_values may be NULL and is not written */
+
+/*
+ * One entry point for every input layout, element format and output variant.
+ *   d_offsets == NULL: fixed-length segments of seg_len elements, as
+ *     radix_topk_batch_topk_half / _bf16 (including k <= seg_len);
+ *   d_offsets != NULL: variable-length segments with seg_len the host-known maximum length,
+ *     as radix_topk_batch_topk_half_segmented / _bf16_segmented.
+ * flags = 0 gives exactly those entry points' results.  RADIX_TOPK_UNSORTED keeps each
+ * row's first min(k, length) slots as the same set of (index, value) entries, in an order
+ * that is unspecified and may differ between calls; the slots past them hold the pad.
+ * It saves the rank counting of long candidate lists.  RADIX_TOPK_INDICES_ONLY writes only
+ * the indices (2 bytes less per output rank).
+ * Rejected (-> 1): an unknown format or flag, NULL d_output_values without
+ * RADIX_TOPK_INDICES_ONLY, and everything the fixed-length or segmented entry point of the
+ * same layout rejects.
+ * No counterpart in the reference, which always writes sorted values and indices
+ * (reference include/batch_topk.cuh:10-19); unsorted and indices-only outputs serve callers
+ * that need neither the order nor the values (a sampler over indices, a set membership).
+ */
+int radix_topk_batch_topk_ex(const void* d_input, int format, const int32_t* d_offsets, int seg_num,
+                             int seg_len, int k, int flags, void* d_output_values,
+                             int32_t* d_output_indices, void* d_workspace, size_t workspace_bytes,
+                             void* stream);
+/* Workspace bytes for radix_topk_batch_topk_ex (segmented != 0: d_offsets given); 0 for an
+ * unsupported shape or format.  Equal to the size of the matching fixed-length or segmented
+ * entry point. */
+size_t radix_topk_batch_topk_ex_workspace_size(int format, int segmented, int seg_num, int seg_len,
+                                               int k);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

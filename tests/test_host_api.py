@@ -146,3 +146,28 @@ def test_sample_validation_rejects_before_any_hip_call():
                     dict(d_topk_indices=0), dict(d_workspace=0), dict(k=0), dict(k=1001),
                     dict(seg_num=0), dict(workspace_bytes=ws - 1)):
             assert fn(**dict(ok, **bad)) == INVALID, (fn.__name__, bad)
+
+
+def test_ex_workspace_matches_the_plain_entry_points():
+    for fmt in (bt.FORMAT_F16, bt.FORMAT_BF16):
+        for shape in ((1, 10000, 50), (128, 128256, 50), (3, 250000, 512), (1, 16777216, 1024)):
+            assert bt.batch_topk_ex_workspace_size(fmt, False, *shape) == bt.batch_topk_half_workspace_size(*shape)
+            assert bt.batch_topk_ex_workspace_size(fmt, True, *shape) == \
+                bt.batch_topk_half_segmented_workspace_size(*shape)
+    assert bt.batch_topk_ex_workspace_size(2, False, 1, 10000, 50) == 0   # unknown format
+    assert bt.batch_topk_ex_workspace_size(bt.FORMAT_F16, False, 1, 10, 11) == 0
+    assert bt.batch_topk_ex_workspace_size(bt.FORMAT_F16, True, 1, 10, 11) > 1  # short segments pad
+
+
+def test_ex_validation_rejects_before_any_hip_call():
+    ws = bt.batch_topk_ex_workspace_size(bt.FORMAT_F16, True, 4, 1000, 64)
+    ok = dict(d_input=P_IN, fmt=bt.FORMAT_F16, d_offsets=P_OFF, seg_num=4, seg_len=1000, k=64, flags=0,
+              d_output_values=P_VAL, d_output_indices=P_IDX, d_workspace=P_WS, workspace_bytes=ws)
+    for bad in (dict(fmt=2), dict(fmt=-1), dict(flags=4), dict(flags=-1),
+                dict(d_output_values=0), dict(d_output_values=0, flags=bt.UNSORTED),
+                dict(d_input=0), dict(d_output_indices=0), dict(d_workspace=0),
+                dict(seg_num=0), dict(seg_len=-1), dict(k=0), dict(k=bt.MAX_K + 1),
+                dict(workspace_bytes=ws - 1), dict(d_input=P_IN + 1), dict(d_output_indices=P_IDX + 2),
+                dict(d_offsets=0, seg_len=10, k=11),   # fixed length: k > seg_len
+                dict(d_offsets=0, seg_len=0)):
+        assert bt.batch_topk_ex(**dict(ok, **bad)) == INVALID, bad
