@@ -42,11 +42,16 @@ EXPORTED_SYMBOLS = (
     "radix_topk_sample_bf16_workspace_size",
     "radix_topk_batch_topk_ex",
     "radix_topk_batch_topk_ex_workspace_size",
+    "radix_topk_batch_topk_f32",
+    "radix_topk_batch_topk_f32_workspace_size",
+    "radix_topk_batch_topk_f32_segmented",
+    "radix_topk_batch_topk_f32_segmented_workspace_size",
 )
 
 # radix_topk_batch_topk_ex element formats and output flags (include/batch_topk.h)
 FORMAT_F16 = 0
 FORMAT_BF16 = 1
+FORMAT_F32 = 2
 UNSORTED = 1
 INDICES_ONLY = 2
 
@@ -94,6 +99,14 @@ def load_library():
             ws = getattr(L, name + "_workspace_size")
             ws.restype = sz
             ws.argtypes = [i32, i32, i32]
+        L.radix_topk_batch_topk_f32.restype = i32
+        L.radix_topk_batch_topk_f32.argtypes = [vp, i32, i32, i32, vp, vp, vp, sz, vp]
+        L.radix_topk_batch_topk_f32_workspace_size.restype = sz
+        L.radix_topk_batch_topk_f32_workspace_size.argtypes = [i32, i32, i32]
+        L.radix_topk_batch_topk_f32_segmented.restype = i32
+        L.radix_topk_batch_topk_f32_segmented.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, sz, vp]
+        L.radix_topk_batch_topk_f32_segmented_workspace_size.restype = sz
+        L.radix_topk_batch_topk_f32_segmented_workspace_size.argtypes = [i32, i32, i32]
         L.radix_topk_batch_topk_ex.restype = i32
         L.radix_topk_batch_topk_ex.argtypes = [vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, sz, vp]
         L.radix_topk_batch_topk_ex_workspace_size.restype = sz
@@ -186,6 +199,31 @@ def sample_bf16_workspace_size(seg_num: int, seg_len: int, k: int) -> int:
     return int(load_library().radix_topk_sample_bf16_workspace_size(seg_num, seg_len, k))
 
 
+def batch_topk_f32(d_input: int, seg_num: int, seg_len: int, k: int, d_output_values: int,
+                   d_output_indices: int, d_workspace: int, workspace_bytes: int,
+                   stream: int = 0) -> int:
+    """radix_topk_batch_topk_f32: fixed-length rows of float (values out as float bits)."""
+    return int(load_library().radix_topk_batch_topk_f32(
+        d_input, seg_num, seg_len, k, d_output_values, d_output_indices, d_workspace,
+        workspace_bytes, stream))
+
+
+def batch_topk_f32_workspace_size(seg_num: int, seg_len: int, k: int) -> int:
+    return int(load_library().radix_topk_batch_topk_f32_workspace_size(seg_num, seg_len, k))
+
+
+def batch_topk_f32_segmented(d_input: int, d_offsets: int, seg_num: int, max_seg_len: int,
+                             k: int, d_output_values: int, d_output_indices: int,
+                             d_workspace: int, workspace_bytes: int, stream: int = 0) -> int:
+    return int(load_library().radix_topk_batch_topk_f32_segmented(
+        d_input, d_offsets, seg_num, max_seg_len, k, d_output_values, d_output_indices,
+        d_workspace, workspace_bytes, stream))
+
+
+def batch_topk_f32_segmented_workspace_size(seg_num: int, max_seg_len: int, k: int) -> int:
+    return int(load_library().radix_topk_batch_topk_f32_segmented_workspace_size(seg_num, max_seg_len, k))
+
+
 def batch_topk_ex(d_input: int, fmt: int, d_offsets: int, seg_num: int, seg_len: int, k: int,
                   flags: int, d_output_values: int, d_output_indices: int, d_workspace: int,
                   workspace_bytes: int, stream: int = 0) -> int:
@@ -213,7 +251,10 @@ def _entry_points(dtype):
     if dtype == torch.bfloat16:
         return (batch_topk_bf16, batch_topk_bf16_workspace_size, batch_topk_bf16_segmented,
                 batch_topk_bf16_segmented_workspace_size)
-    raise ValueError(f"unsupported dtype {dtype}: float16 or bfloat16")
+    if dtype == torch.float32:
+        return (batch_topk_f32, batch_topk_f32_workspace_size, batch_topk_f32_segmented,
+                batch_topk_f32_segmented_workspace_size)
+    raise ValueError(f"unsupported dtype {dtype}: float16, bfloat16 or float32")
 
 def _stream_handle(stream) -> int:
     import torch
@@ -229,7 +270,9 @@ def _format_of(dtype) -> int:
         return FORMAT_F16
     if dtype == torch.bfloat16:
         return FORMAT_BF16
-    raise ValueError(f"unsupported dtype {dtype}: float16 or bfloat16")
+    if dtype == torch.float32:
+        return FORMAT_F32
+    raise ValueError(f"unsupported dtype {dtype}: float16, bfloat16 or float32")
 
 
 def _topk_ex(x, offsets, seg_num, seg_len, k, sorted, values, workspace, stream):
@@ -253,7 +296,7 @@ def _topk_ex(x, offsets, seg_num, seg_len, k, sorted, values, workspace, stream)
 
 
 def topk(x, k: int, workspace=None, stream=None, sorted: bool = True, values: bool = True):
-    """Top-k of every row of a contiguous float16 or bfloat16 CUDA tensor [seg_num, seg_len].
+    """Top-k of every row of a contiguous float16, bfloat16 or float32 CUDA tensor [seg_num, seg_len].
 
     Returns (values [seg_num, k] of x's dtype, indices int32 [seg_num, k]).  ``workspace``
     may be a uint8 CUDA tensor of at least the workspace size of the shape.  ``sorted=False``
@@ -262,7 +305,7 @@ def topk(x, k: int, workspace=None, stream=None, sorted: bool = True, values: bo
     import torch
 
     if x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
-        raise ValueError("topk expects a contiguous 2-D float16 or bfloat16 CUDA tensor")
+        raise ValueError("topk expects a contiguous 2-D float16, bfloat16 or float32 CUDA tensor")
     if not (sorted and values):
         return _topk_ex(x, None, x.shape[0], x.shape[1], k, sorted, values, workspace, stream)
     fixed, fixed_ws, _, _ = _entry_points(x.dtype)
@@ -283,8 +326,8 @@ def topk(x, k: int, workspace=None, stream=None, sorted: bool = True, values: bo
 
 def segmented_topk(x, offsets, k: int, max_seg_len: int, workspace=None, stream=None,
                    sorted: bool = True, values: bool = True):
-    """Top-k of every segment x[offsets[s]:offsets[s+1]] of a 1-D float16 or bfloat16 CUDA
-    tensor.
+    """Top-k of every segment x[offsets[s]:offsets[s+1]] of a 1-D float16, bfloat16 or float32
+    CUDA tensor.
 
     ``offsets`` is an int32 CUDA tensor of seg_num + 1 entries.  Ranks beyond a segment's
     length hold index -1 and value bits 0xFFFF.  ``sorted`` and ``values`` as for topk.
@@ -292,7 +335,7 @@ def segmented_topk(x, offsets, k: int, max_seg_len: int, workspace=None, stream=
     import torch
 
     if not x.is_cuda or not x.is_contiguous():
-        raise ValueError("segmented_topk expects a contiguous float16 or bfloat16 CUDA tensor")
+        raise ValueError("segmented_topk expects a contiguous float16, bfloat16 or float32 CUDA tensor")
     if offsets.dtype != torch.int32 or not offsets.is_cuda or offsets.dim() != 1:
         raise ValueError("offsets must be a 1-D int32 CUDA tensor")
     if not (sorted and values):

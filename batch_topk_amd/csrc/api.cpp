@@ -35,8 +35,12 @@ int next_pow2(int x) {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Launch plan for segments of at most `max_len` elements (plus up to 7 elements of
-// misalignment of the 16-byte load grid), `seg_num` segments and `k` outputs each.
+// Launch plan for segments of at most `max_len` elements (plus up to ev - 1 elements of
+// misalignment of the 16-byte load grid), `seg_num` segments and `k` outputs each, for
+// elements of which one 16-byte vector holds `ev` (8 for 16-bit formats, 4 for fp32).
+// `shared_alignment`: fixed-length rows that all start at the input pointer's alignment (one
+// row, or a length that is a whole number of vectors), so that the launch knows the exact
+// aligned span of every row.
 //
 // The workgroup shape has at least 4k threads so each wave's share of k stays well below its
 // 64 lanes; the rest of the choice depends on how many segments share a CU (below).  Longer segments are split into
@@ -44,12 +48,12 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // the W lists fit one workgroup's LDS merge area.  Beyond that (long segments with large k)
 // the segment's W workgroups run cooperatively: all co-resident, they build one
 // whole-segment threshold from global histograms and a single candidate list.
-Plan make_plan(int seg_num, int64_t max_len, int k) {
+Plan make_plan(int seg_num, int64_t max_len, int k, int ev = 8, bool shared_alignment = false) {
   Plan plan{};
   plan.ok = false;
   if (seg_num <= 0 || k <= 0 || k > kMaxK || max_len < 0) return plan;
   const int block_min = k <= 64 ? 256 : (k <= 128 ? 512 : 1024);
-  const int64_t span = max_len + 7;  // worst-case aligned span of one segment
+  const int64_t span = max_len + ev - 1;  // worst-case aligned span of one segment
   int block = 1024, vpt = 16;
   bool found = false;
   if (seg_num >= 2 * kPlanCUs) {
@@ -59,7 +63,7 @@ Plan make_plan(int seg_num, int64_t max_len, int k) {
     // whose misaligned span reaches past the chunk takes a second (tail) workgroup.
     for (int cb = block_min > 512 ? block_min : 512; cb <= 1024 && !found; cb *= 2) {
       for (int cv : {2, 4, 8, 16}) {
-        if (!found && static_cast<int64_t>(cb) * cv * 8 >= max_len) {
+        if (!found && static_cast<int64_t>(cb) * cv * ev >= max_len) {
           block = cb;
           vpt = cv;
           found = true;
@@ -71,7 +75,7 @@ Plan make_plan(int seg_num, int64_t max_len, int k) {
     // thread (then the fewest threads) that covers the whole aligned span.
     for (int cv : {2, 4, 8, 16}) {
       for (int cb = block_min; cb <= 1024 && !found; cb *= 2) {
-        if (static_cast<int64_t>(cb) * cv * 8 >= span) {
+        if (static_cast<int64_t>(cb) * cv * ev >= span) {
           block = cb;
           vpt = cv;
           found = true;
@@ -80,14 +84,18 @@ Plan make_plan(int seg_num, int64_t max_len, int k) {
       if (found) break;
     }
   }
-  const int chunk = block * vpt * 8;
+  const int chunk = block * vpt * ev;
   const int64_t W = span <= chunk ? 1 : (span + chunk - 1) / chunk;
   const int kpad = next_pow2(k < 64 ? 64 : k);
   int cap_list = W > 1 ? next_pow2(2 * k > 128 ? 2 * k : 128) : 0;
   bool cooperative = false;
   if (W > 1 && W * static_cast<int64_t>(cap_list) > kCandArea) {
-    // Too many lists to merge in LDS: cooperative path, if the grid can be co-resident.
-    if (static_cast<int64_t>(seg_num) * W > kMaxCoopGroups) return plan;
+    // Too many lists to merge in LDS: cooperative path, if the grid can be co-resident.  The
+    // workspace covers the worst-case misalignment (W chunks).  Rows of a shared alignment
+    // launch with their exact chunk count, ceil(max_len / chunk) when 16-byte aligned (a
+    // misaligned pointer that needs more co-resident workgroups is refused at launch).
+    const int64_t w_launch = shared_alignment ? (max_len + chunk - 1) / chunk : W;
+    if (static_cast<int64_t>(seg_num) * w_launch > kMaxCoopGroups) return plan;
     cooperative = true;
     cap_list = 0;
   }
@@ -144,25 +152,37 @@ struct SampleSpec {
   float inv_temperature;
 };
 
-int run(const Plan& plan, uint32_t inf_bits, const uint16_t* d_input, const int32_t* d_offsets,
-        int seg_num, int64_t seg_len, int64_t max_len, int k, uint16_t* d_values, int32_t* d_indices,
+int run(const Plan& plan, uint32_t inf_bits, const void* d_input, const int32_t* d_offsets,
+        int seg_num, int64_t seg_len, int64_t max_len, int k, void* d_values, int32_t* d_indices,
         void* d_workspace, size_t workspace_bytes, void* stream, const SampleSpec* sample = nullptr,
         bool unsorted = false) {
   if (!plan.ok || workspace_bytes < plan.ws_bytes) return kInvalid;
   const uintptr_t in_addr = reinterpret_cast<uintptr_t>(d_input);
-  if ((in_addr & 1u) || (reinterpret_cast<uintptr_t>(d_values) & 1u) ||
+  const uintptr_t eb = inf_bits == kInfBitsF32 ? 4u : 2u;  // element bytes
+  if ((in_addr % eb) || (reinterpret_cast<uintptr_t>(d_values) % eb) ||
       (reinterpret_cast<uintptr_t>(d_indices) & 3u) || (reinterpret_cast<uintptr_t>(d_offsets) & 3u)) {
     return kInvalid;
   }
   TopkParams p{};
   p.base = reinterpret_cast<const uint16_t*>(in_addr & ~static_cast<uintptr_t>(15));
-  p.elem0 = static_cast<int64_t>((in_addr & 15u) >> 1);
+  p.elem0 = static_cast<int64_t>((in_addr & 15u) / eb);
+  p.elem_bytes = static_cast<int32_t>(eb);
   p.offsets = d_offsets;
   p.seg_len = seg_len;
   p.max_len = max_len;
   p.seg_num = seg_num;
   p.k = k;
   p.chunks_per_seg = plan.W;
+  if (plan.cooperative && !d_offsets) {
+    // Fixed-length rows that all share the input pointer's alignment (one row, or a length
+    // that is a whole number of 16-byte vectors): the exact aligned span decides the chunk
+    // count, so an aligned row does not pay a workgroup for the worst-case misalignment.
+    const int64_t ev = 16 / static_cast<int64_t>(eb);
+    if (seg_num == 1 || seg_len % ev == 0) {
+      const int64_t span = p.elem0 + seg_len;
+      p.chunks_per_seg = static_cast<int32_t>((span + plan.chunk - 1) / plan.chunk);
+    }
+  }
   p.cap_chunk = plan.cap_chunk;
   p.cap_list = plan.cap_list;
   p.cand_area = plan.cand_area;
@@ -195,7 +215,7 @@ int run(const Plan& plan, uint32_t inf_bits, const uint16_t* d_input, const int3
   const int rc = launch_segmented_topk(plan, p, stream);
   if (rc != 0 || !sample || !plan.cooperative) return rc;
   SampleParams sp{};
-  sp.topk_vals = d_values;
+  sp.topk_vals = static_cast<const uint16_t*>(d_values);
   sp.topk_idx = d_indices;
   sp.uniforms = sample->uniforms;
   sp.samples = sample->samples;
@@ -207,46 +227,63 @@ int run(const Plan& plan, uint32_t inf_bits, const uint16_t* d_input, const int3
   return launch_topk_sample(sp, stream);
 }
 
-size_t fixed_workspace_size(int seg_num, int seg_len, int k) {
+// Elements per 16-byte vector of the format whose +inf pattern is `inf_bits`.
+int ev_of(uint32_t inf_bits) { return inf_bits == kInfBitsF32 ? 4 : 8; }
+
+// Fixed-length rows that all start at the input pointer's alignment.
+bool shared_alignment(int seg_num, int64_t seg_len, uint32_t inf_bits) {
+  return seg_num == 1 || seg_len % ev_of(inf_bits) == 0;
+}
+
+size_t fixed_workspace_size(int seg_num, int seg_len, int k, uint32_t inf_bits = kInfBitsF16) {
   if (seg_num <= 0 || seg_len <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K || k > seg_len) return 0;
-  const Plan plan = make_plan(seg_num, seg_len, k);
+  const Plan plan =
+      make_plan(seg_num, seg_len, k, ev_of(inf_bits), shared_alignment(seg_num, seg_len, inf_bits));
   return plan.ok ? plan.ws_bytes : 0;
 }
 
-int fixed_topk(uint32_t inf_bits, const uint16_t* d_input, int seg_num, int seg_len, int k,
-               uint16_t* d_output_values, int32_t* d_output_indices, void* d_workspace,
+int fixed_topk(uint32_t inf_bits, const void* d_input, int seg_num, int seg_len, int k,
+               void* d_output_values, int32_t* d_output_indices, void* d_workspace,
                size_t workspace_bytes, void* stream) {
   if (seg_num <= 0 || seg_len <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K || k > seg_len) return kInvalid;
   if (!d_input || !d_output_values || !d_output_indices || !d_workspace) return kInvalid;
-  const Plan plan = make_plan(seg_num, seg_len, k);
+  const Plan plan =
+      make_plan(seg_num, seg_len, k, ev_of(inf_bits), shared_alignment(seg_num, seg_len, inf_bits));
   return run(plan, inf_bits, d_input, nullptr, seg_num, seg_len, seg_len, k, d_output_values,
              d_output_indices, d_workspace, workspace_bytes, stream);
 }
 
-size_t segmented_workspace_size(int seg_num, int max_seg_len, int k) {
+size_t segmented_workspace_size(int seg_num, int max_seg_len, int k, uint32_t inf_bits = kInfBitsF16) {
   if (seg_num <= 0 || max_seg_len < 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return 0;
-  const Plan plan = make_plan(seg_num, max_seg_len, k);
+  const Plan plan = make_plan(seg_num, max_seg_len, k, ev_of(inf_bits));
   return plan.ok ? plan.ws_bytes : 0;
 }
 
-int segmented_topk(uint32_t inf_bits, const uint16_t* d_input, const int32_t* d_offsets, int seg_num,
-                   int max_seg_len, int k, uint16_t* d_output_values, int32_t* d_output_indices,
+int segmented_topk(uint32_t inf_bits, const void* d_input, const int32_t* d_offsets, int seg_num,
+                   int max_seg_len, int k, void* d_output_values, int32_t* d_output_indices,
                    void* d_workspace, size_t workspace_bytes, void* stream) {
   if (seg_num <= 0 || max_seg_len < 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return kInvalid;
   if (!d_input || !d_offsets || !d_output_values || !d_output_indices || !d_workspace) return kInvalid;
-  const Plan plan = make_plan(seg_num, max_seg_len, k);
+  const Plan plan = make_plan(seg_num, max_seg_len, k, ev_of(inf_bits));
   return run(plan, inf_bits, d_input, d_offsets, seg_num, 0, max_seg_len, k, d_output_values,
              d_output_indices, d_workspace, workspace_bytes, stream);
 }
 
 // Extended entry point: element format, fixed-length or segmented input, output flags.
 bool known_format(int format) {
-  return format == RADIX_TOPK_FORMAT_F16 || format == RADIX_TOPK_FORMAT_BF16;
+  return format == RADIX_TOPK_FORMAT_F16 || format == RADIX_TOPK_FORMAT_BF16 ||
+         format == RADIX_TOPK_FORMAT_F32;
+}
+
+uint32_t inf_of(int format) {
+  return format == RADIX_TOPK_FORMAT_F32 ? kInfBitsF32
+                                         : (format == RADIX_TOPK_FORMAT_BF16 ? kInfBitsBF16 : kInfBitsF16);
 }
 
 size_t ex_workspace_size(int format, int segmented, int seg_num, int seg_len, int k) {
   if (!known_format(format)) return 0;
-  return segmented ? segmented_workspace_size(seg_num, seg_len, k) : fixed_workspace_size(seg_num, seg_len, k);
+  return segmented ? segmented_workspace_size(seg_num, seg_len, k, inf_of(format))
+                   : fixed_workspace_size(seg_num, seg_len, k, inf_of(format));
 }
 
 int topk_ex(const void* d_input, int format, const int32_t* d_offsets, int seg_num, int seg_len, int k,
@@ -258,10 +295,11 @@ int topk_ex(const void* d_input, int format, const int32_t* d_offsets, int seg_n
   if (seg_num <= 0 || k <= 0 || k > RADIX_TOPK_MAX_K) return kInvalid;
   if (d_offsets ? seg_len < 0 : (seg_len <= 0 || k > seg_len)) return kInvalid;
   if (!d_input || !d_output_indices || !d_workspace || (!indices_only && !d_output_values)) return kInvalid;
-  const Plan plan = make_plan(seg_num, seg_len, k);
-  const uint32_t inf = format == RADIX_TOPK_FORMAT_BF16 ? kInfBitsBF16 : kInfBitsF16;
-  uint16_t* vals = indices_only ? nullptr : static_cast<uint16_t*>(d_output_values);
-  return run(plan, inf, static_cast<const uint16_t*>(d_input), d_offsets, seg_num, d_offsets ? 0 : seg_len,
+  const uint32_t inf = inf_of(format);
+  const Plan plan =
+      make_plan(seg_num, seg_len, k, ev_of(inf), !d_offsets && shared_alignment(seg_num, seg_len, inf));
+  void* vals = indices_only ? nullptr : d_output_values;
+  return run(plan, inf, d_input, d_offsets, seg_num, d_offsets ? 0 : seg_len,
              seg_len, k, vals, d_output_indices, d_workspace, workspace_bytes, stream, nullptr,
              (flags & RADIX_TOPK_UNSORTED) != 0);
 }
@@ -277,7 +315,7 @@ int sample_topk(bool bf16, const uint16_t* d_logits, int seg_num, int seg_len, i
   if (!d_uniforms || !d_samples) return kInvalid;
   const float inv_t = 1.0f / temperature;
   if (!std::isfinite(inv_t)) return kInvalid;
-  const Plan plan = make_plan(seg_num, seg_len, k);
+  const Plan plan = make_plan(seg_num, seg_len, k, 8, shared_alignment(seg_num, seg_len, kInfBitsF16));
   const SampleSpec spec{d_uniforms, d_samples, d_probs, inv_t};
   return run(plan, bf16 ? kInfBitsBF16 : kInfBitsF16, d_logits, nullptr, seg_num, seg_len, seg_len, k,
              d_topk_values, d_topk_indices, d_workspace, workspace_bytes, stream, &spec);
@@ -338,6 +376,31 @@ int radix_topk_batch_topk_bf16_segmented(const uint16_t* d_input, const int32_t*
                                          void* stream) {
   return radix_topk_amd::segmented_topk(kInfBitsBF16, d_input, d_offsets, seg_num, max_seg_len, k,
                                         d_output_values, d_output_indices, d_workspace,
+                                        workspace_bytes, stream);
+}
+
+size_t radix_topk_batch_topk_f32_workspace_size(int seg_num, int seg_len, int k) {
+  return radix_topk_amd::fixed_workspace_size(seg_num, seg_len, k, radix_topk_amd::kInfBitsF32);
+}
+
+int radix_topk_batch_topk_f32(const float* d_input, int seg_num, int seg_len, int k, float* d_output_values,
+                              int32_t* d_output_indices, void* d_workspace, size_t workspace_bytes,
+                              void* stream) {
+  return radix_topk_amd::fixed_topk(radix_topk_amd::kInfBitsF32, d_input, seg_num, seg_len, k,
+                                    d_output_values, d_output_indices, d_workspace, workspace_bytes,
+                                    stream);
+}
+
+size_t radix_topk_batch_topk_f32_segmented_workspace_size(int seg_num, int max_seg_len, int k) {
+  return radix_topk_amd::segmented_workspace_size(seg_num, max_seg_len, k, radix_topk_amd::kInfBitsF32);
+}
+
+int radix_topk_batch_topk_f32_segmented(const float* d_input, const int32_t* d_offsets, int seg_num,
+                                        int max_seg_len, int k, float* d_output_values,
+                                        int32_t* d_output_indices, void* d_workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return radix_topk_amd::segmented_topk(radix_topk_amd::kInfBitsF32, d_input, d_offsets, seg_num,
+                                        max_seg_len, k, d_output_values, d_output_indices, d_workspace,
                                         workspace_bytes, stream);
 }
 

@@ -28,9 +28,11 @@ constexpr int kMaxChunk = 1024 * 16 * 8;
 //                                     spread over kGroupCopies copies so that few workgroups
 //                                     add to one address
 //   fine    u32 [kFineCopies][2048]   the same thread bests at 32-key resolution (key >> 5)
-//   rhist   u32 [6][256]              refinement digit histograms
+//   rhist   u32 [kRefineDigits][256]  refinement digit histograms (6 digits of a 16-bit key and
+//                                     a 32-bit index, 8 with a 32-bit key)
 //   lists   u64 [W][kCandArea]        every workgroup's candidate list
-constexpr int kGroupBarriers = 10;
+constexpr int kRefineDigits = 8;
+constexpr int kGroupBarriers = 3 + kRefineDigits;
 constexpr int kGroupCopies = 16;
 constexpr int kFineCopies = 8;
 constexpr int kFineBins = 2048;
@@ -56,7 +58,7 @@ constexpr GroupLayout group_layout(int W) {
   L.fine = off;
   off += static_cast<size_t>(kFineCopies) * kFineBins * 4;
   L.rhist = off;
-  off += static_cast<size_t>(6) * 256 * 4;
+  off += static_cast<size_t>(kRefineDigits) * 256 * 4;
   L.lists = off;
   off += static_cast<size_t>(W) * kCandArea * 8;
   L.bytes = off;
@@ -69,6 +71,8 @@ constexpr int kMaxCoopGroups = 256;
 // +inf bit patterns of the two 16-bit element formats; a magnitude above it is a NaN.
 constexpr uint32_t kInfBitsF16 = 0x7C00u;
 constexpr uint32_t kInfBitsBF16 = 0x7F80u;
+// +inf of fp32; passed as the format tag of the 32-bit element path.
+constexpr uint32_t kInfBitsF32 = 0x7F800000u;
 
 // Kernel parameter block of the fused segmented top-k kernel.  Every segment s covers the
 // element range [s0, s1) of `base` (a 16-byte aligned pointer); s0/s1 come from the int32
@@ -88,14 +92,15 @@ struct TopkParams {
   int32_t cand_area;            // LDS entries of the candidate / merge area
   int32_t kpad;                 // LDS entries of the selection area (power of two >= k)
   int32_t cooperative;          // 1: whole-segment threshold across the segment's workgroups
-  uint16_t* out_vals;           // [seg_num, k], or nullptr: indices only
+  void* out_vals;               // [seg_num, k] element bits (2 or 4 bytes), or nullptr: indices only
   int32_t unsorted;             // 1: each row's selected set in unspecified order
   int32_t* out_idx;             // [seg_num, k]
   unsigned long long* tickets;  // [seg_num] arrival words (epoch << 16 | count)
   int32_t* list_counts;         // [seg_num * W]
   unsigned long long* lists;    // [seg_num * W * cap_list] packed (key16 << 32 | index)
   unsigned long long epoch;     // 48-bit token unique to this call
-  uint32_t inf_bits;            // +inf pattern of the 16-bit element format (0x7C00 fp16, 0x7F80 bf16)
+  uint32_t inf_bits;            // +inf pattern of a 16-bit element format (0x7C00 fp16, 0x7F80 bf16)
+  int32_t elem_bytes;           // 2 (fp16, bf16) or 4 (fp32)
   // Top-k sampling fused into the last step (non-cooperative plans), off when samples is null.
   const float* uniforms;        // [seg_num] u in [0, 1)
   int32_t* samples;             // [seg_num] sampled index (-1 for an empty segment)

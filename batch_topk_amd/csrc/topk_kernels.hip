@@ -48,6 +48,7 @@
 #include <atomic>
 #include <cstdint>
 #include <cstdlib>
+#include <type_traits>
 
 #include "sample_row.hpp"
 #include "topk_common.hpp"
@@ -103,6 +104,52 @@ __device__ __forceinline__ u64 pack_candidate(u32 raw, u32 index, u32 inf) {
 }
 __device__ __forceinline__ u32 cand_index(u64 P) { return static_cast<u32>(P >> 16); }
 __device__ __forceinline__ u32 cand_raw(u64 P) { return static_cast<u32>(P) & 0xffffu; }
+
+// The same key for raw fp32 bits: NaN -> 0xFFFFFFFF, +-0 -> 0x7FFFFFFF, negative -> bits,
+// positive -> bits ^ 0x7FFFFFFF.
+__device__ __forceinline__ u32 desc_key32(u32 b) {
+  const u32 mag = b & 0x7fffffffu;
+  u32 key = (b & 0x80000000u) ? b : (b ^ 0x7fffffffu);
+  key = (mag == 0u) ? 0x7fffffffu : key;
+  key = (mag > 0x7f800000u) ? 0xffffffffu : key;
+  return key;
+}
+
+// Element formats.  The kernel is written once for 16-bit and 32-bit elements.  Thread bests,
+// threshold histograms and the filter bound always work on 16-bit key prefixes; candidates
+// carry the exact key, so the selection among them is exact.
+//   Elem16 (fp16, bf16; the +inf pattern comes at run time): 8 elements per 16-byte vector,
+//     candidate = key16 << 48 | index << 16 | raw16.
+//   Elem32 (fp32): 4 elements per vector, candidate = key32 << 32 | index.  The top 16 bits
+//     of the key order like the key, so every element of a row's top k passes a threshold on
+//     them; the raw bits of an output entry are decoded from its key (re-read from the input
+//     for +-0 and NaN, whose keys merge several patterns).
+struct Elem16 {
+  static constexpr int kPerVec = 8;
+  static constexpr int kBytes = 2;
+  static constexpr int kKeyBits = 16;
+  static constexpr int kIdxShift = 16;  // index field of a candidate
+  static constexpr int kLowDigit = 16;  // radix digits below this never tell candidates apart
+  __device__ static u32 key(u32 b, u32 inf) { return desc_key(b, inf); }
+  __device__ static u32 prefix(u32 b, u32 inf) { return desc_key(b, inf); }
+  __device__ static u64 pack(u32 b, u32 idx, u32 inf) { return pack_candidate(b, idx, inf); }
+  __device__ static u32 index(u64 P) { return cand_index(P); }
+  __device__ static u32 element(const u32 (&w4)[4], int e) { return (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu; }
+  __device__ static void fill(u32 (&w4)[4], int e) { w4[e >> 1] |= 0xffffu << ((e & 1) * 16); }
+};
+struct Elem32 {
+  static constexpr int kPerVec = 4;
+  static constexpr int kBytes = 4;
+  static constexpr int kKeyBits = 32;
+  static constexpr int kIdxShift = 0;
+  static constexpr int kLowDigit = 0;
+  __device__ static u32 key(u32 b, u32) { return desc_key32(b); }
+  __device__ static u32 prefix(u32 b, u32) { return desc_key32(b) >> 16; }
+  __device__ static u64 pack(u32 b, u32 idx, u32) { return (static_cast<u64>(desc_key32(b)) << 32) | idx; }
+  __device__ static u32 index(u64 P) { return static_cast<u32>(P); }
+  __device__ static u32 element(const u32 (&w4)[4], int e) { return w4[e]; }
+  __device__ static void fill(u32 (&w4)[4], int e) { w4[e] = 0xffffffffu; }
+};
 
 // ------------------------------------------------------------------------------ wave64 helpers
 
@@ -228,14 +275,14 @@ __device__ __forceinline__ void wave_find_bucket(const u32* hist, int need, int*
 // Exact radix select over M unique packed values in LDS: returns the bound B such that
 // exactly kk values are <= B (1 <= kk <= M).  8-bit digits over the key and index fields,
 // MSB first, early exit as soon as a bucket is taken whole.
-template <int BLOCK>
+template <int BLOCK, class E>
 __device__ u64 block_select_bound(const u64* list, int M, int kk, u32* hist, int* scal) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = tid >> 6;
   u64 prefix = 0, pmask = 0;
   int need = kk;
-  for (int shift = 56; shift >= 16; shift -= 8) {
+  for (int shift = 56; shift >= E::kLowDigit; shift -= 8) {
     for (int i = tid; i < 256; i += BLOCK) hist[i] = 0;
     __syncthreads();
     for (int i = tid; i < M; i += BLOCK) {
@@ -256,24 +303,49 @@ __device__ u64 block_select_bound(const u64* list, int M, int kk, u32* hist, int
   return prefix | ~pmask;
 }
 
-// Writes the pad (index -1, value bits 0xFFFF) at output slot o; indices-only calls have no
-// value array.
+// Writes the pad (index -1, all-ones value bits: a NaN) at output slot o; indices-only calls
+// have no value array.
+template <class E>
 __device__ __forceinline__ void write_pad(const TopkParams& p, int64_t o) {
   p.out_idx[o] = -1;
-  if (p.out_vals) p.out_vals[o] = 0xffffu;
+  if (p.out_vals) {
+    if constexpr (E::kBytes == 2) {
+      static_cast<uint16_t*>(p.out_vals)[o] = 0xffffu;
+    } else {
+      static_cast<u32*>(p.out_vals)[o] = 0xffffffffu;
+    }
+  }
+}
+
+// Raw fp32 bits of a candidate: decoded from its key, except for the keys of +-0 and NaN,
+// which merge several bit patterns; those are read back from the input.
+__device__ __forceinline__ u32 raw32_of(const TopkParams& p, int seg, u32 idx, u64 P) {
+  const u32 key = static_cast<u32>(P >> 32);
+  if (key == 0xffffffffu || key == 0x7fffffffu) {
+    const int64_t s0 = (p.offsets ? static_cast<int64_t>(p.offsets[seg]) : static_cast<int64_t>(seg) * p.seg_len) + p.elem0;
+    return reinterpret_cast<const u32*>(p.base)[s0 + idx];
+  }
+  return (key & 0x80000000u) ? key : (key ^ 0x7fffffffu);
 }
 
 // Writes rank r of the segment's output row.  An entry outside the segment (only a padding
 // sentinel can be) is written as the pad.
+template <class E>
 __device__ __forceinline__ void write_rank(const TopkParams& p, int64_t n, int seg, int r, u64 P) {
-  const u32 idx = cand_index(P);
+  const u32 idx = E::index(P);
   const int64_t o = static_cast<int64_t>(seg) * p.k + r;
   if (r >= p.k) return;
   if (static_cast<int64_t>(idx) < n) {
     p.out_idx[o] = static_cast<int>(idx);
-    if (p.out_vals) p.out_vals[o] = static_cast<uint16_t>(cand_raw(P));
+    if (p.out_vals) {
+      if constexpr (E::kBytes == 2) {
+        static_cast<uint16_t*>(p.out_vals)[o] = static_cast<uint16_t>(cand_raw(P));
+      } else {
+        static_cast<u32*>(p.out_vals)[o] = raw32_of(p, seg, idx, P);
+      }
+    }
   } else {
-    write_pad(p, o);
+    write_pad<E>(p, o);
   }
 }
 
@@ -305,7 +377,7 @@ __device__ void block_rank(const u64* v, int M, int* rank) {
 // Ranks the M (<= 64 * S) unique candidates of `list` and stores those of rank < kk at
 // sel[rank].  Every wave holds the whole list in registers (S u64 per lane) and ranks its
 // share of the candidates with ballots: rank(x) = sum over slots of popcount(ballot(c < x)).
-template <int BLOCK, int S>
+template <int BLOCK, int S, class E>
 __device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
                                 int kk, u64* sorted) {
   constexpr int NW = BLOCK / 64;
@@ -341,7 +413,7 @@ __device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u
   }
   TOPK_WTRACE(7);
   if (lane < count && my_rank < kk) {
-    write_rank(p, n, seg, my_rank, mine);
+    write_rank<E>(p, n, seg, my_rank, mine);
     if (sorted) sorted[my_rank] = mine;
   }
 }
@@ -351,7 +423,7 @@ __device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u
 // row (16 lanes) per candidate: lane q of the row compares it with entries q, q + 16, ... (held
 // in registers, loaded once), and a row prefix sum leaves its rank in the row's last lane,
 // which writes the output entry.  The rows take the candidates in turn.
-template <int BLOCK>
+template <int BLOCK, class E>
 __device__ void row_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M, int kk,
                                u64* sorted) {
   constexpr int ROWS = BLOCK / 16;
@@ -375,7 +447,7 @@ __device__ void row_rank_write(const TopkParams& p, int64_t n, int seg, const u6
     cnt += dpp<0x114, 0xf>(cnt);
     cnt += dpp<0x118, 0xf>(cnt);
     if (q == 15 && cnt < static_cast<u32>(kk)) {
-      write_rank(p, n, seg, static_cast<int>(cnt), x);
+      write_rank<E>(p, n, seg, static_cast<int>(cnt), x);
       if (sorted) sorted[cnt] = x;
     }
   }
@@ -401,42 +473,42 @@ __device__ __forceinline__ void sample_segment(const TopkParams& p, const u64* s
 // list is longer than 128 (shorter lists are ranked anyway: the ranking is the selection).
 // With top-k sampling on, the ranked entries are also kept in LDS (sm.sel, or sm.area when
 // sm.sel holds the selection) and wave 0 then draws the segment's sample.
-template <int BLOCK>
+template <int BLOCK, class E>
 __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int kk, int64_t n,
                                  int seg) {
   const int tid = threadIdx.x;
   if (M < kk) kk = M;  // cannot happen (every candidate list holds >= kk entries); keeps it safe
   for (int r = kk + tid; r < p.k; r += BLOCK) {
     const int64_t o = static_cast<int64_t>(seg) * p.k + r;
-    write_pad(p, o);
+    write_pad<E>(p, o);
   }
-  const bool sampling = p.samples != nullptr;
+  const bool sampling = E::kBytes == 2 && p.samples != nullptr;  // 16-bit formats only
   constexpr int NW = BLOCK / 64;
   u64* sorted = sm.sel;
   // Small sets: one DPP row per candidate counts the smaller entries (row_rank_write).
   if (M <= 128) {
-    row_rank_write<BLOCK>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+    row_rank_write<BLOCK, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
   } else if (p.unsorted && !sampling) {
     // Unsorted output: the kk best, found by radix select, in the order they are found.
     if (M > kk) {
-      const u64 bound = block_select_bound<BLOCK>(sm.area, M, kk, sm.hist, sm.scal);
+      const u64 bound = block_select_bound<BLOCK, E>(sm.area, M, kk, sm.hist, sm.scal);
       if (tid == 0) sm.scal[3] = 0;
       __syncthreads();
       for (int i = tid; i < M; i += BLOCK) {
         const u64 P = sm.area[i];
-        if (P <= bound) write_rank(p, n, seg, atomicAdd(&sm.scal[3], 1), P);
+        if (P <= bound) write_rank<E>(p, n, seg, atomicAdd(&sm.scal[3], 1), P);
       }
     } else {
-      for (int i = tid; i < M; i += BLOCK) write_rank(p, n, seg, i, sm.area[i]);
+      for (int i = tid; i < M; i += BLOCK) write_rank<E>(p, n, seg, i, sm.area[i]);
     }
   } else if (NW >= 8 && M <= 8 * NW * 4 && M <= 512) {
     // Up to 512: every wave ranks its share against the whole list held in registers (a
     // radix select first costs more: tied keys take it through the index digits).
-    if constexpr (NW >= 8) wave_rank_write<BLOCK, 8>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+    if constexpr (NW >= 8) wave_rank_write<BLOCK, 8, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
   } else {
     const u64* sel = sm.area;
     if (M > kk) {
-      const u64 bound = block_select_bound<BLOCK>(sm.area, M, kk, sm.hist, sm.scal);
+      const u64 bound = block_select_bound<BLOCK, E>(sm.area, M, kk, sm.hist, sm.scal);
       if (tid == 0) sm.scal[3] = 0;
       __syncthreads();
       for (int i = tid; i < M; i += BLOCK) {
@@ -452,13 +524,15 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
     }
     block_rank<BLOCK>(sel, kk, sm.rank);
     for (int i = tid; i < kk; i += BLOCK) {
-      write_rank(p, n, seg, sm.rank[i], sel[i]);
+      write_rank<E>(p, n, seg, sm.rank[i], sel[i]);
       if (sampling) sorted[sm.rank[i]] = sel[i];
     }
   }
-  if (sampling) {
-    __syncthreads();
-    sample_segment(p, sorted, kk, seg);
+  if constexpr (E::kBytes == 2) {
+    if (sampling) {
+      __syncthreads();
+      sample_segment(p, sorted, kk, seg);
+    }
   }
 }
 
@@ -497,9 +571,11 @@ __device__ __forceinline__ u64 pair_mark(u64 epoch, int w) {
 // Published entries carry a tag in bits 18..31 of their index field (two-chunk segments have
 // indices below 2^18) with the top bit set, which no plain index has; the length word carries
 // a 16-bit tag with the top bit set above the length.
-constexpr u64 kPairTagMask = 0x3fffull << 34;
+template <class E>
+constexpr u64 pair_tag_mask() { return 0x3fffull << (E::kIdxShift + 18); }
+template <class E>
 __device__ __forceinline__ u64 pair_entry_tag(u64 epoch) {
-  return (0x2000ull | (epoch & 0x1fffu)) << 34;
+  return (0x2000ull | (epoch & 0x1fffu)) << (E::kIdxShift + 18);
 }
 __device__ __forceinline__ u32 pair_count_tag(u64 epoch) {
   return 0x8000u | static_cast<u32>(epoch & 0x7fffu);
@@ -702,7 +778,7 @@ __device__ u32 group_collect(const u64* counts, const u64* lists, u64 tag, int a
 // Ranks the candidates list[c0, c1) against all M unique entries of `list` (LDS) and writes
 // those of rank < kk to the output row: one wave per candidate, each lane comparing every
 // 64th entry, the counts summed across the wave.
-template <int BLOCK>
+template <int BLOCK, class E>
 __device__ void rank_range_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
                                  int kk, int c0, int c1) {
   constexpr int NW = BLOCK / 64;
@@ -713,7 +789,7 @@ __device__ void rank_range_write(const TopkParams& p, int64_t n, int seg, const 
     u32 c = 0;
     for (int j = lane; j < M; j += 64) c += list[j] < P ? 1u : 0u;
     const u32 r = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_scan(c)), 63));
-    if (lane == 0 && r < static_cast<u32>(kk)) write_rank(p, n, seg, static_cast<int>(r), P);
+    if (lane == 0 && r < static_cast<u32>(kk)) write_rank<E>(p, n, seg, static_cast<int>(r), P);
   }
 }
 
@@ -721,6 +797,19 @@ __device__ __forceinline__ short2_t as_s2(u32 w) { return __builtin_bit_cast(sho
 __device__ __forceinline__ u32 as_u32(short2_t w) { return __builtin_bit_cast(u32, w); }
 
 // Packed int16 max / min of the 8 halves of a vector, as the two halves of one word.
+__device__ __forceinline__ int vec_max4_i32(const uint4& x) {
+  const int a = static_cast<int>(x.x) > static_cast<int>(x.y) ? static_cast<int>(x.x) : static_cast<int>(x.y);
+  const int b = static_cast<int>(x.z) > static_cast<int>(x.w) ? static_cast<int>(x.z) : static_cast<int>(x.w);
+  return a > b ? a : b;
+}
+__device__ __forceinline__ int vec_min4_i32(const uint4& x) {
+  const int a = static_cast<int>(x.x) < static_cast<int>(x.y) ? static_cast<int>(x.x) : static_cast<int>(x.y);
+  const int b = static_cast<int>(x.z) < static_cast<int>(x.w) ? static_cast<int>(x.z) : static_cast<int>(x.w);
+  return a < b ? a : b;
+}
+// Largest int value of a per-vector max (either half of a packed pair, or the int32 itself).
+__device__ __forceinline__ int vec_gmax(short2_t g) { return g.x > g.y ? g.x : g.y; }
+__device__ __forceinline__ int vec_gmax(int g) { return g; }
 __device__ __forceinline__ u32 vec_max2(const uint4& x) {
   return as_u32(__builtin_elementwise_max(__builtin_elementwise_max(as_s2(x.x), as_s2(x.y)),
                                           __builtin_elementwise_max(as_s2(x.z), as_s2(x.w))));
@@ -734,11 +823,12 @@ __device__ __forceinline__ u32 vec_min2(const uint4& x) {
 
 // At least 4 waves per SIMD (at most 128 VGPRs): one 1024-thread workgroup, or two 512-thread
 // ones, per CU.  (Fewer, fatter waves -- 512 threads x 32 vectors -- measured slower.)
-template <int BLOCK, int VPT, bool COOP>
+template <int BLOCK, int VPT, bool COOP, class E>
 __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
 segmented_topk_kernel(TopkParams p) {
   constexpr int NW = BLOCK / 64;
-  constexpr int CH = BLOCK * VPT * 8;
+  constexpr int EV = E::kPerVec;  // elements per 16-byte vector
+  constexpr int CH = BLOCK * VPT * EV;
   static_assert(CH <= 65536 * 2, "chunk positions must fit the refinement packing, and the "
                                  "indices of a two-chunk segment 18 bits");
   static_assert(NW <= 16, "at most 16 waves");
@@ -769,7 +859,7 @@ segmented_topk_kernel(TopkParams p) {
   s0 += p.elem0;
   s1 += p.elem0;
   const int64_t n = s1 - s0;
-  const int64_t a0 = s0 & ~static_cast<int64_t>(7);
+  const int64_t a0 = s0 & ~static_cast<int64_t>(EV - 1);
   const int64_t span_aligned = s1 - a0;
   const int64_t Ws64 = n > 0 ? (span_aligned + CH - 1) / CH : 0;
 
@@ -779,9 +869,11 @@ segmented_topk_kernel(TopkParams p) {
     if (w == 0) {
       for (int r = tid; r < k; r += BLOCK) {
         const int64_t o = static_cast<int64_t>(seg) * k + r;
-        write_pad(p, o);
+        write_pad<E>(p, o);
       }
-      if (!COOP && p.samples) sample_segment(p, nullptr, 0, seg);
+      if constexpr (!COOP && E::kBytes == 2) {
+        if (p.samples) sample_segment(p, nullptr, 0, seg);
+      }
     }
     return;
   }
@@ -811,7 +903,7 @@ segmented_topk_kernel(TopkParams p) {
     if (w == 0) {
       for (int i = tid; i < kGroupCopies * 256; i += BLOCK) store_agent(g.hist + i, 0u);
       for (int i = tid; i < kFineCopies * kFineBins; i += BLOCK) store_agent(g.fine + i, 0u);
-      for (int i = tid; i < 6 * 256; i += BLOCK) store_agent(g.rhist + i, 0u);
+      for (int i = tid; i < kRefineDigits * 256; i += BLOCK) store_agent(g.rhist + i, 0u);
       wait_vector_memory();
       __syncthreads();
       if (tid == 0) store_agent(g.flag, (tag << 20) | 1u);
@@ -824,10 +916,11 @@ segmented_topk_kernel(TopkParams p) {
   // boundary at or past hi, so a vector wholly past the chunk reads as zero without touching
   // memory; the vector holding hi is read whole, as the refinement re-read below also does.
   uint4 v[VPT];
-  const unsigned char* cptr = reinterpret_cast<const unsigned char*>(p.base + cb);
+  const unsigned char* cptr = reinterpret_cast<const unsigned char*>(p.base) + cb * E::kBytes;
   {
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<unsigned char*>(cptr), static_cast<short>(0), ((hi + 7) & ~7) * 2, kBufferWord3);
+        const_cast<unsigned char*>(cptr), static_cast<short>(0), ((hi + EV - 1) & ~(EV - 1)) * E::kBytes,
+        kBufferWord3);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, tid * 16, j * BLOCK * 16, kCachePolicyNT);
@@ -857,38 +950,61 @@ segmented_topk_kernel(TopkParams p) {
   // past hi is workgroup-uniform, so the per-lane test runs only for those vectors.
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    if ((j == 0 && lo > 0) || (j + 1) * BLOCK * 8 > hi) {
-      const int pos = (j * BLOCK + tid) * 8;
-      if (pos < lo || pos + 8 > hi) {
+    if ((j == 0 && lo > 0) || (j + 1) * BLOCK * EV > hi) {
+      const int pos = (j * BLOCK + tid) * EV;
+      if (pos < lo || pos + EV > hi) {
         u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (pos + e < lo || pos + e >= hi) w4[e >> 1] |= 0xffffu << ((e & 1) * 16);
+        for (int e = 0; e < EV; ++e) {
+          if (pos + e < lo || pos + e >= hi) E::fill(w4, e);
         }
         v[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
       }
     }
   }
 
-  // ---- 2. thread best (packed int16 max tree).  As int16, the non-negative-sign halves
-  // order like their values, so the int16 max is the thread's best unless it has none: then
-  // its best is the int16 min (the negative value nearest zero), and only a wave holding such
-  // a lane builds the min tree.  Every VALU instruction here costs all 4 waves of the SIMD.
-  short2_t gv[VPT];  // per-vector packed max, kept for the filter's vector test
+  // ---- 2. thread best (packed int16 max tree; for 32-bit elements an int32 one).  As
+  // signed integers, the non-negative-sign elements order like their values, so the max is
+  // the thread's best unless it has none: then its best is the min (the negative value
+  // nearest zero), and only a wave holding such a lane builds the min tree.  Every VALU
+  // instruction here costs all 4 waves of the SIMD.
+  using VecMax = std::conditional_t<E::kBytes == 2, short2_t, int>;
+  VecMax gv[VPT];  // per-vector max, kept for the filter's vector test
+  int m1, m2;
+  if constexpr (E::kBytes == 2) {
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) gv[j] = as_s2(vec_max2(v[j]));
-  short2_t mx = gv[0];
+    for (int j = 0; j < VPT; ++j) gv[j] = as_s2(vec_max2(v[j]));
+    short2_t mx = gv[0];
 #pragma unroll
-  for (int j = 1; j < VPT; ++j) mx = __builtin_elementwise_max(mx, gv[j]);
-  const int m1 = mx.x > mx.y ? mx.x : mx.y;  // int16 max: the best non-negative-sign half
-  int m2 = 32767;
-  if (ballot(m1 < 0)) {
-    short2_t mn = as_s2(vec_min2(v[0]));
+    for (int j = 1; j < VPT; ++j) mx = __builtin_elementwise_max(mx, gv[j]);
+    m1 = mx.x > mx.y ? mx.x : mx.y;  // int16 max: the best non-negative-sign half
+    m2 = 32767;
+    if (ballot(m1 < 0)) {
+      short2_t mn = as_s2(vec_min2(v[0]));
 #pragma unroll
-    for (int j = 1; j < VPT; ++j) mn = __builtin_elementwise_min(mn, as_s2(vec_min2(v[j])));
-    m2 = mn.x < mn.y ? mn.x : mn.y;
+      for (int j = 1; j < VPT; ++j) mn = __builtin_elementwise_min(mn, as_s2(vec_min2(v[j])));
+      m2 = mn.x < mn.y ? mn.x : mn.y;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) gv[j] = vec_max4_i32(v[j]);
+    int mx = gv[0];
+#pragma unroll
+    for (int j = 1; j < VPT; ++j) mx = mx > gv[j] ? mx : gv[j];
+    m1 = mx;
+    m2 = 0x7fffffff;
+    if (ballot(m1 < 0)) {
+      int mn = vec_min4_i32(v[0]);
+#pragma unroll
+      for (int j = 1; j < VPT; ++j) {
+        const int t = vec_min4_i32(v[j]);
+        mn = mn < t ? mn : t;
+      }
+      m2 = mn;
+    }
   }
-  const u32 best_key = desc_key(static_cast<u32>(m1 >= 0 ? m1 : m2) & 0xffffu, inf);
+  const u32 best_bits = static_cast<u32>(m1 >= 0 ? m1 : m2) & (E::kBytes == 2 ? 0xffffu : 0xffffffffu);
+  const u32 best_key = E::prefix(best_bits, inf);
   TOPK_TRACE(1);
   TOPK_WTRACE(1);
 
@@ -961,8 +1077,9 @@ segmented_topk_kernel(TopkParams p) {
   TOPK_TRACE(4);
   TOPK_WTRACE(0);
 
-  // ---- 4. filter {key <= T} into the contiguous LDS candidate list, packed as
-  // (key16 << 48 | index32 << 16 | raw16).  Instruction counts matter more than latency here:
+  // ---- 4. filter {key prefix <= T} into the contiguous LDS candidate list, packed as
+  // (key16 << 48 | index32 << 16 | raw16), or (key32 << 32 | index32) for 32-bit elements.
+  // Instruction counts matter more than latency here:
   // the 16 waves of a CU share its scalar unit and LDS, and each SIMD issues for 4 waves.
   const bool all_mode = T == 0xffffu;  // no usable threshold: fewer than kc bests, or NaNs
   // Each thread best with key <= T is an element with key <= T: when more of them exist than
@@ -979,10 +1096,11 @@ segmented_topk_kernel(TopkParams p) {
     // subtract d = b - raw(T) per word and two unsigned compares give the exact hits
     // (d <= inf - raw(T) holds exactly for raw(T) <= b <= inf).  A wave prefix sum
     // gives every hit its offset, and one LDS atomic per 64 staged vectors reserves the
-    // wave's slots in the list.
-    const u32 t_lo = T ^ 0x7fffu;
+    // wave's slots in the list.  For 32-bit elements the bound is raw(T) << 16 (the smallest
+    // positive pattern whose key prefix is T) and the test one unsigned compare per word.
+    const u32 t_lo = E::kBytes == 2 ? (T ^ 0x7fffu) : ((T ^ 0x7fffu) << 16);
     const ushort2_t tt = {static_cast<unsigned short>(t_lo), static_cast<unsigned short>(t_lo)};
-    const u32 span = inf - t_lo;
+    const u32 span = (E::kBytes == 2 ? inf : 0x7f800000u) - t_lo;
     const u32 span_hi = (span << 16) | 0xffffu;
     uint4* st_vec = reinterpret_cast<uint4*>(sm.stage + wid * kStageWords);
     u32* st_pos = sm.stage + wid * kStageWords + 256;
@@ -992,7 +1110,7 @@ segmented_topk_kernel(TopkParams p) {
     auto flush = [&]() {
       wave_lds_sync();
       u32 w4[4] = {0u, 0u, 0u, 0u};
-      u32 hm = 0;  // hits among the 8 halves of this lane's staged vector
+      u32 hm = 0;  // hits among the elements of this lane's staged vector
       u32 p0 = 0;
       if (static_cast<u32>(lane) < nst) {
         const uint4 x = st_vec[lane];
@@ -1000,9 +1118,13 @@ segmented_topk_kernel(TopkParams p) {
         p0 = idx_base + st_pos[lane];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const u32 d = __builtin_bit_cast(u32, __builtin_bit_cast(ushort2_t, w4[q]) - tt);
-          hm |= static_cast<u32>(static_cast<unsigned short>(d) <= span) << (2 * q);
-          hm |= static_cast<u32>(d <= span_hi) << (2 * q + 1);
+          if constexpr (E::kBytes == 2) {
+            const u32 d = __builtin_bit_cast(u32, __builtin_bit_cast(ushort2_t, w4[q]) - tt);
+            hm |= static_cast<u32>(static_cast<unsigned short>(d) <= span) << (2 * q);
+            hm |= static_cast<u32>(d <= span_hi) << (2 * q + 1);
+          } else {
+            hm |= static_cast<u32>(w4[q] - t_lo <= span) << q;
+          }
         }
       }
       const u32 cnt = static_cast<u32>(__builtin_popcount(hm));
@@ -1015,11 +1137,16 @@ segmented_topk_kernel(TopkParams p) {
         while (hm) {
           const u32 e = static_cast<u32>(__builtin_ctz(hm));
           hm &= hm - 1u;
-          const u32 word = e < 2u ? w4[0] : (e < 4u ? w4[1] : (e < 6u ? w4[2] : w4[3]));
-          const u32 b = (word >> ((e & 1u) * 16u)) & 0xffffu;
           const u32 pi = p0 + e;
-          if (o < static_cast<u32>(kArea))
-            sm.area[o] = (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b);
+          if constexpr (E::kBytes == 2) {
+            const u32 word = e < 2u ? w4[0] : (e < 4u ? w4[1] : (e < 6u ? w4[2] : w4[3]));
+            const u32 b = (word >> ((e & 1u) * 16u)) & 0xffffu;
+            if (o < static_cast<u32>(kArea))
+              sm.area[o] = (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b);
+          } else {
+            const u32 b = e == 0u ? w4[0] : (e == 1u ? w4[1] : (e == 2u ? w4[2] : w4[3]));
+            if (o < static_cast<u32>(kArea)) sm.area[o] = (static_cast<u64>(b ^ 0x7fffffffu) << 32) | pi;
+          }
           ++o;
         }
       }
@@ -1029,8 +1156,7 @@ segmented_topk_kernel(TopkParams p) {
     // Stage the passing vectors: one compare and ballot per vector gives the wave's passing
     // lanes, and a wave-uniform branch skips the vectors no lane passes.
     auto stage_vector = [&](int j) {  // inlined into unrolled loops: j is a constant
-      const int gmax = gv[j].x > gv[j].y ? gv[j].x : gv[j].y;
-      const bool mine = gmax >= static_cast<int>(t_lo);
+      const bool mine = vec_gmax(gv[j]) >= static_cast<int>(t_lo);
       const u64 m = ballot(mine);
       if (m) {
         const u32 c = static_cast<u32>(__popcll(m));
@@ -1038,7 +1164,7 @@ segmented_topk_kernel(TopkParams p) {
         if (mine) {
           const u32 slot = nst + mbcnt(m);
           st_vec[slot] = v[j];
-          st_pos[slot] = static_cast<u32>((j * BLOCK + tid) * 8);
+          st_pos[slot] = static_cast<u32>((j * BLOCK + tid) * EV);
         }
         nst += c;
       }
@@ -1050,7 +1176,8 @@ segmented_topk_kernel(TopkParams p) {
     TOPK_WTRACE(4);
   } else if (filter) {
     // T is +-0 or negative: candidates are every non-NaN positive and the b with
-    // uint16(b) <= raw(T) (raw of the zero class taken as 0x8000).  Each wave collects its hits
+    // uint16(b) <= raw(T) (raw of the zero class taken as 0x8000); for 32-bit elements, the
+    // b whose key prefix is <= T.  Each wave collects its hits
     // in a private LDS region (ballot/mbcnt slots), then reserves its share of the list with
     // one LDS atomic and copies the region there.
     constexpr int RC = kStageWords / 2;  // region capacity (u64 entries) per wave
@@ -1061,15 +1188,20 @@ segmented_topk_kernel(TopkParams p) {
     for (int j = 0; j < VPT; ++j) {
       const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        const bool h = b <= traw && (b & 0x7fffu) <= inf;
+      for (int e = 0; e < EV; ++e) {
+        const u32 b = E::element(w4, e);
+        bool h;
+        if constexpr (E::kBytes == 2) {
+          h = b <= traw && (b & 0x7fffu) <= inf;
+        } else {
+          h = E::prefix(b, inf) <= T;
+        }
         const u64 m = ballot(h);
         if (m) {
           if (h) {
             const u32 slot = wcount + mbcnt(m);
             if (slot < static_cast<u32>(RC))
-              region[slot] = pack_candidate(b, idx_base + static_cast<u32>((j * BLOCK + tid) * 8 + e), inf);
+              region[slot] = E::pack(b, idx_base + static_cast<u32>((j * BLOCK + tid) * EV + e), inf);
           }
           wcount += static_cast<u32>(__popcll(m));
         }
@@ -1104,14 +1236,14 @@ segmented_topk_kernel(TopkParams p) {
   auto for_each_element = [&](auto&& fn) {
 #pragma unroll 1
     for (int j = 0; j < VPT; ++j) {
-      const int pos0 = (j * BLOCK + tid) * 8;
-      if (pos0 < hi && pos0 + 8 > lo) {
-        const uint4 x = *reinterpret_cast<const uint4*>(cptr + static_cast<u32>(pos0) * 2u);
+      const int pos0 = (j * BLOCK + tid) * EV;
+      if (pos0 < hi && pos0 + EV > lo) {
+        const uint4 x = *reinterpret_cast<const uint4*>(cptr + static_cast<u32>(pos0) * E::kBytes);
         const u32 w4[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int e = 0; e < EV; ++e) {
           const int pos = pos0 + e;
-          if (pos >= lo && pos < hi) fn((w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu, pos);
+          if (pos >= lo && pos < hi) fn(E::element(w4, e), pos);
         }
       }
     }
@@ -1136,19 +1268,20 @@ segmented_topk_kernel(TopkParams p) {
     u32 total = group_collect<BLOCK>(g.counts, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20);
     if (total == kAbsent) {
       // ---- 4d. the list would not fit: exact radix refinement over the whole segment of
-      // Q = key16 << 32 | index32 among the elements with key <= T, one global histogram per
-      // 8-bit digit, until at most kCandArea elements are <= the bound (so that any one
+      // Q = key << 32 | index32 among the elements with key prefix <= T, one global histogram
+      // per 8-bit digit, until at most kCandArea elements are <= the bound (so that any one
       // workgroup's share fits its own list).
       u64 prefix = 0, pmask = 0;
       int rneed = kk;
       int pass = 0;
-      for (int shift = 40; shift >= 0; shift -= 8, ++pass) {
+      constexpr u64 kQMask = E::kKeyBits == 32 ? ~0ull : ((1ull << (32 + E::kKeyBits)) - 1);
+      static_assert(E::kKeyBits / 8 + 4 <= kRefineDigits, "one histogram per digit of Q");
+      for (int shift = E::kKeyBits + 24; shift >= 0; shift -= 8, ++pass) {
         for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
         __syncthreads();
         for_each_element([&](u32 b, int pos) {
-          const u32 key = desc_key(b, inf);
-          const u64 Q = (static_cast<u64>(key) << 32) | (idx_base + static_cast<u32>(pos));
-          if (key <= T && (Q & pmask) == prefix) atomicAdd(&sm.hist[(Q >> shift) & 255u], 1u);
+          const u64 Q = (static_cast<u64>(E::key(b, inf)) << 32) | (idx_base + static_cast<u32>(pos));
+          if (E::prefix(b, inf) <= T && (Q & pmask) == prefix) atomicAdd(&sm.hist[(Q >> shift) & 255u], 1u);
         });
         __syncthreads();
         group_histogram_single<BLOCK>(sm.hist, g.rhist + pass * 256, g.arrive + (3 + pass) * W, epoch, w, Ws);
@@ -1163,16 +1296,15 @@ segmented_topk_kernel(TopkParams p) {
         pmask |= 0xffull << shift;
         if ((kk - rneed) + cnt_b <= kCandArea) break;  // fits every workgroup's own list
       }
-      const u64 bound = prefix | (~pmask & 0xFFFFFFFFFFFFull);
+      const u64 bound = prefix | (~pmask & kQMask);
       if (tid == 0) sm.scal[4] = 0;
       __syncthreads();
       for_each_element([&](u32 b, int pos) {
-        const u32 key = desc_key(b, inf);
         const u32 idx = idx_base + static_cast<u32>(pos);
-        const u64 Q = (static_cast<u64>(key) << 32) | idx;
-        if (key <= T && Q <= bound) {
+        const u64 Q = (static_cast<u64>(E::key(b, inf)) << 32) | idx;
+        if (E::prefix(b, inf) <= T && Q <= bound) {
           const int slot = atomicAdd(&sm.scal[4], 1);
-          if (slot < kArea) sm.area[slot] = pack_candidate(b, idx, inf);
+          if (slot < kArea) sm.area[slot] = E::pack(b, idx, inf);
         }
       });
       __syncthreads();
@@ -1188,13 +1320,13 @@ segmented_topk_kernel(TopkParams p) {
     if (w == 0) {
       for (int r = kk + tid; r < k; r += BLOCK) {
         const int64_t o = static_cast<int64_t>(seg) * k + r;
-        write_pad(p, o);
+        write_pad<E>(p, o);
       }
     }
     const int per = (static_cast<int>(total) + Ws - 1) / Ws;
     const int c0 = w * per < static_cast<int>(total) ? w * per : static_cast<int>(total);
     const int c1 = c0 + per < static_cast<int>(total) ? c0 + per : static_cast<int>(total);
-    rank_range_write<BLOCK>(p, n, seg, sm.area, static_cast<int>(total), kk, c0, c1);
+    rank_range_write<BLOCK, E>(p, n, seg, sm.area, static_cast<int>(total), kk, c0, c1);
     TOPK_TRACE(11);
     return;
   }
@@ -1204,28 +1336,27 @@ segmented_topk_kernel(TopkParams p) {
     for (int j = 0; j < VPT; ++j) {
       const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int pos = (j * BLOCK + tid) * 8 + e;
-        const u32 b = (w4[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        if (pos >= lo && pos < hi) sm.area[pos - lo] = pack_candidate(b, idx_base + static_cast<u32>(pos), inf);
+      for (int e = 0; e < EV; ++e) {
+        const int pos = (j * BLOCK + tid) * EV + e;
+        const u32 b = E::element(w4, e);
+        if (pos >= lo && pos < hi) sm.area[pos - lo] = E::pack(b, idx_base + static_cast<u32>(pos), inf);
       }
     }
     C = nc;
     __syncthreads();
   } else if (all_mode || overflow) {
     // ---- 4b. exact refinement (rare: ties or NaN-dominated rows overflow the LDS list).
-    // Radix select over P = key16 << 17 | position17 among in-range elements with key <= T,
-    // until at most kArea values are <= the bound.  The chunk is re-read from memory for each
-    // pass, so the registers of the fast path are not kept live for it.
+    // Radix select over P = key << 17 | position17 among in-range elements with key prefix
+    // <= T, until at most kArea values are <= the bound.  The chunk is re-read from memory for
+    // each pass, so the registers of the fast path are not kept live for it.
     u64 prefix = 0, pmask = 0;
     int need = kc;
-    for (int shift = 32; shift >= 0; shift -= 8) {
+    for (int shift = E::kKeyBits + 16; shift >= 0; shift -= 8) {
       for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
       __syncthreads();
       for_each_element([&](u32 b, int pos) {
-        const u32 key = desc_key(b, inf);
-        const u64 P = (static_cast<u64>(key) << 17) | static_cast<u32>(pos);
-        if (key <= T && (P & pmask) == prefix) atomicAdd(&sm.hist[(P >> shift) & 255u], 1u);
+        const u64 P = (static_cast<u64>(E::key(b, inf)) << 17) | static_cast<u32>(pos);
+        if (E::prefix(b, inf) <= T && (P & pmask) == prefix) atomicAdd(&sm.hist[(P >> shift) & 255u], 1u);
       });
       __syncthreads();
       if (wid == 0) wave_find_bucket(sm.hist, need, sm.scal, lane);
@@ -1239,15 +1370,14 @@ segmented_topk_kernel(TopkParams p) {
       const int count_le = (kc - need) + cnt;
       if (count_le <= kArea) break;
     }
-    const u64 bound = prefix | (~pmask & 0x1FFFFFFFFull);
+    const u64 bound = prefix | (~pmask & ((1ull << (E::kKeyBits + 17)) - 1));
     if (tid == 0) sm.scal[4] = 0;
     __syncthreads();
     for_each_element([&](u32 b, int pos) {
-      const u32 key = desc_key(b, inf);
-      const u64 P = (static_cast<u64>(key) << 17) | static_cast<u32>(pos);
-      if (key <= T && P <= bound) {
+      const u64 P = (static_cast<u64>(E::key(b, inf)) << 17) | static_cast<u32>(pos);
+      if (E::prefix(b, inf) <= T && P <= bound) {
         const int slot = atomicAdd(&sm.scal[4], 1);
-        if (slot < kArea) sm.area[slot] = pack_candidate(b, idx_base + static_cast<u32>(pos), inf);
+        if (slot < kArea) sm.area[slot] = E::pack(b, idx_base + static_cast<u32>(pos), inf);
       }
     });
     __syncthreads();
@@ -1265,7 +1395,7 @@ segmented_topk_kernel(TopkParams p) {
     const u64* src = sm.area;
     int M = C;
     if (C > p.cap_list) {
-      const u64 bound = block_select_bound<BLOCK>(sm.area, C, kc, sm.hist, sm.scal);
+      const u64 bound = block_select_bound<BLOCK, E>(sm.area, C, kc, sm.hist, sm.scal);
       if (tid == 0) sm.scal[3] = 0;
       __syncthreads();
       for (int i = tid; i < C; i += BLOCK) {
@@ -1286,7 +1416,8 @@ segmented_topk_kernel(TopkParams p) {
       // own list, polling until the length and every entry carry the tag, then clears the
       // consumed words (so a replay with the same epoch cannot take them for fresh ones) and
       // the ticket.
-      const u64 etag = pair_entry_tag(epoch);
+      const u64 etag = pair_entry_tag<E>(epoch);
+    constexpr u64 kPairTagMask = pair_tag_mask<E>();
       const u32 ctag = pair_count_tag(epoch);
       if (!sm.scal[5]) {
         const int64_t my_id = static_cast<int64_t>(seg) * W + w;
@@ -1371,14 +1502,14 @@ segmented_topk_kernel(TopkParams p) {
   }
 
   // ---- 6. select and write the segment's row
-  finalize_segment<BLOCK>(p, sm, Mf, kk, n, seg);
+  finalize_segment<BLOCK, E>(p, sm, Mf, kk, n, seg);
   TOPK_TRACE(11);
 }
 
-template <int BLOCK, int VPT>
+template <int BLOCK, int VPT, class E>
 int launch_shape(const Plan& plan, const TopkParams& params, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(params.seg_num) * plan.W));
-  hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT, false>), grid, dim3(BLOCK),
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(params.seg_num) * params.chunks_per_seg));
+  hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT, false, E>), grid, dim3(BLOCK),
                      static_cast<unsigned>(plan.lds_bytes), stream, params);
   return static_cast<int>(hipGetLastError());
 }
@@ -1412,46 +1543,53 @@ bool formal_cooperative_launch() {
   return on;
 }
 
+template <class E>
 int launch_cooperative(const Plan& plan, TopkParams params, hipStream_t stream) {
-  const int64_t groups = static_cast<int64_t>(params.seg_num) * plan.W;
+  const int64_t groups = static_cast<int64_t>(params.seg_num) * params.chunks_per_seg;
   if (groups > device_cu_count()) return static_cast<int>(hipErrorCooperativeLaunchTooLarge);
   const dim3 grid(static_cast<unsigned>(groups));
   if (formal_cooperative_launch()) {
     void* args[] = {&params};
     const hipError_t e = hipLaunchCooperativeKernel(
-        reinterpret_cast<const void*>(&segmented_topk_kernel<1024, 16, true>), grid, dim3(1024), args,
+        reinterpret_cast<const void*>(&segmented_topk_kernel<1024, 16, true, E>), grid, dim3(1024), args,
         static_cast<unsigned>(plan.lds_bytes), stream);
     if (e != hipSuccess) return static_cast<int>(e);
   } else {
-    hipLaunchKernelGGL((segmented_topk_kernel<1024, 16, true>), grid, dim3(1024),
+    hipLaunchKernelGGL((segmented_topk_kernel<1024, 16, true, E>), grid, dim3(1024),
                        static_cast<unsigned>(plan.lds_bytes), stream, params);
   }
   return static_cast<int>(hipGetLastError());
+}
+
+// The instantiation for the plan's workgroup shape and element format.
+template <class E>
+int launch_format(const Plan& plan, const TopkParams& params, hipStream_t s) {
+  const int b = plan.shape.block;
+  const int vpt = plan.shape.vpt;
+  if (plan.cooperative) {
+    if (b != 1024 || vpt != 16) return static_cast<int>(hipErrorInvalidValue);
+    return launch_cooperative<E>(plan, params, s);
+  }
+  if (b == 256 && vpt == 2) return launch_shape<256, 2, E>(plan, params, s);
+  if (b == 256 && vpt == 4) return launch_shape<256, 4, E>(plan, params, s);
+  if (b == 256 && vpt == 8) return launch_shape<256, 8, E>(plan, params, s);
+  if (b == 256 && vpt == 16) return launch_shape<256, 16, E>(plan, params, s);
+  if (b == 512 && vpt == 2) return launch_shape<512, 2, E>(plan, params, s);
+  if (b == 512 && vpt == 4) return launch_shape<512, 4, E>(plan, params, s);
+  if (b == 512 && vpt == 8) return launch_shape<512, 8, E>(plan, params, s);
+  if (b == 512 && vpt == 16) return launch_shape<512, 16, E>(plan, params, s);
+  if (b == 1024 && vpt == 2) return launch_shape<1024, 2, E>(plan, params, s);
+  if (b == 1024 && vpt == 4) return launch_shape<1024, 4, E>(plan, params, s);
+  if (b == 1024 && vpt == 8) return launch_shape<1024, 8, E>(plan, params, s);
+  if (b == 1024 && vpt == 16) return launch_shape<1024, 16, E>(plan, params, s);
+  return static_cast<int>(hipErrorInvalidValue);
 }
 
 }  // namespace
 
 int launch_segmented_topk(const Plan& plan, const TopkParams& params, void* stream) {
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const int b = plan.shape.block;
-  const int vpt = plan.shape.vpt;
-  if (plan.cooperative) {
-    if (b != 1024 || vpt != 16) return static_cast<int>(hipErrorInvalidValue);
-    return launch_cooperative(plan, params, s);
-  }
-  if (b == 256 && vpt == 2) return launch_shape<256, 2>(plan, params, s);
-  if (b == 256 && vpt == 4) return launch_shape<256, 4>(plan, params, s);
-  if (b == 256 && vpt == 8) return launch_shape<256, 8>(plan, params, s);
-  if (b == 256 && vpt == 16) return launch_shape<256, 16>(plan, params, s);
-  if (b == 512 && vpt == 2) return launch_shape<512, 2>(plan, params, s);
-  if (b == 512 && vpt == 4) return launch_shape<512, 4>(plan, params, s);
-  if (b == 512 && vpt == 8) return launch_shape<512, 8>(plan, params, s);
-  if (b == 512 && vpt == 16) return launch_shape<512, 16>(plan, params, s);
-  if (b == 1024 && vpt == 2) return launch_shape<1024, 2>(plan, params, s);
-  if (b == 1024 && vpt == 4) return launch_shape<1024, 4>(plan, params, s);
-  if (b == 1024 && vpt == 8) return launch_shape<1024, 8>(plan, params, s);
-  if (b == 1024 && vpt == 16) return launch_shape<1024, 16>(plan, params, s);
-  return static_cast<int>(hipErrorInvalidValue);
+  return params.elem_bytes == 4 ? launch_format<Elem32>(plan, params, s) : launch_format<Elem16>(plan, params, s);
 }
 
 }  // namespace radix_topk_amd

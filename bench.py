@@ -18,13 +18,15 @@ Prints ONE JSON line:
 Other workloads (--workload uniform_small | ties_special | varlen | huge_segment, and
 ref_matrix --seg-num N for the reference's own benchmark matrix) print the same line for
 that configuration.  --dtype bf16 runs the bfloat16 entry points on the same workload
-rounded to bfloat16 (no CPU baseline: that is the reference's fp16 verifier).  --op sample
+rounded to bfloat16 (no CPU baseline: that is the reference's fp16 verifier); --dtype f32 the
+float32 entry points on the workload widened to float32 (the same values; 4 bytes per element
+in the algorithmic bytes).  --op sample
 times the top-k sampling consumer (radix_topk_sample_*: the top-k, then one draw per row
 from the softmax of its top-k at --temperature) on fixed-length workloads.  --output times an
 output variant of radix_topk_batch_topk_ex (unsorted rows, indices only, or both); its
 algorithmic bytes count 4 bytes per output rank when no values are written.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--k K] [--dtype f16|bf16]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--k K] [--dtype f16|bf16|f32]
                        [--op topk|sample] [--output sorted|unsorted|indices|unsorted-indices]
 """
 
@@ -129,7 +131,7 @@ def main() -> int:
     ap.add_argument("--rotate-mb", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
-    ap.add_argument("--dtype", choices=("f16", "bf16"), default="f16")
+    ap.add_argument("--dtype", choices=("f16", "bf16", "f32"), default="f16")
     ap.add_argument("--op", choices=("topk", "sample"), default="topk")
     ap.add_argument("--temperature", type=float, default=1.0)
     ap.add_argument("--output", choices=("sorted", "unsorted", "indices", "unsorted-indices"),
@@ -150,11 +152,14 @@ def main() -> int:
     k = args.k
     if args.op == "sample" and offsets_of(args.workload):
         raise SystemExit("--op sample runs on fixed-length workloads")
+    if args.op == "sample" and args.dtype == "f32":
+        raise SystemExit("--op sample takes 16-bit logits")
     flags = {"sorted": 0, "unsorted": bt.UNSORTED, "indices": bt.INDICES_ONLY,
              "unsorted-indices": bt.UNSORTED | bt.INDICES_ONLY}[args.output]
     if flags and args.op == "sample":
         raise SystemExit("--output applies to --op topk")
-    ex_format = bt.FORMAT_F16 if args.dtype == "f16" else bt.FORMAT_BF16
+    ex_format = {"f16": bt.FORMAT_F16, "bf16": bt.FORMAT_BF16, "f32": bt.FORMAT_F32}[args.dtype]
+    elem_bytes = 4 if args.dtype == "f32" else 2
     if args.dtype == "bf16":
         # the same workload rounded to bfloat16 (round to nearest even)
         bits = torch.from_numpy(bits.view(np.float16).astype(np.float32)).bfloat16() \
@@ -162,6 +167,12 @@ def main() -> int:
         cfg["workload"] += ", rounded to bfloat16"
         fixed, fixed_ws = bt.batch_topk_bf16, bt.batch_topk_bf16_workspace_size
         seg, seg_ws = bt.batch_topk_bf16_segmented, bt.batch_topk_bf16_segmented_workspace_size
+    elif args.dtype == "f32":
+        # the same workload widened to float32 (exact: the same values, the same top-k)
+        bits = bits.view(np.float16).astype(np.float32).view(np.uint32)
+        cfg["workload"] += ", widened to float32"
+        fixed, fixed_ws = bt.batch_topk_f32, bt.batch_topk_f32_workspace_size
+        seg, seg_ws = bt.batch_topk_f32_segmented, bt.batch_topk_f32_segmented_workspace_size
     else:
         fixed, fixed_ws = bt.batch_topk_half, bt.batch_topk_half_workspace_size
         seg, seg_ws = bt.batch_topk_half_segmented, bt.batch_topk_half_segmented_workspace_size
@@ -179,10 +190,10 @@ def main() -> int:
     in_bytes = bits.nbytes
     copies = max(1, -(-args.rotate_mb * 2**20 // in_bytes))
     log(f"workload {cfg['workload']} k={k}, {copies} input copies ({copies * in_bytes / 2**20:.0f} MB)")
-    src = torch.from_numpy(bits.view(np.int16)).to(dev)
+    src = torch.from_numpy(bits.view(np.int32 if elem_bytes == 4 else np.int16)).to(dev)
     inputs = [src] + [src.clone() for _ in range(copies - 1)]
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    vals = torch.empty((seg_num, k), dtype=torch.int16, device=dev)
+    vals = torch.empty((seg_num, k), dtype=torch.int32 if elem_bytes == 4 else torch.int16, device=dev)
     idx = torch.empty((seg_num, k), dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
@@ -226,7 +237,7 @@ def main() -> int:
         ev, ei = O.batch_topk_half(bits[:int(offsets[8])], k, offsets=offsets[:9].astype(np.int64),
                                    fmt=args.dtype)
     gi = idx.cpu().numpy()[:8]
-    gv = vals.cpu().numpy().view(np.uint16)[:8]
+    gv = vals.cpu().numpy().view(np.uint32 if elem_bytes == 4 else np.uint16)[:8]
     if flags & bt.UNSORTED:
         # the same (index, value) set per row, in any order (pads: index -1 sorts first)
         go, eo = np.argsort(gi, axis=1, kind="stable"), np.argsort(ei, axis=1, kind="stable")
@@ -263,10 +274,10 @@ def main() -> int:
     warm_us = per_launch(100, False)
     kern_us = float(np.median(cold_us))
 
-    # Algorithmic bytes: every input element read once (2 B), every output rank written once
-    # (2 B value + 4 B index), plus the offsets array when given.
-    out_bytes = 4 if flags & bt.INDICES_ONLY else 6
-    alg_bytes = 2 * n_elements + out_bytes * seg_num * k + (0 if offsets is None else 4 * (seg_num + 1))
+    # Algorithmic bytes: every input element read once (2 B, 4 B for fp32), every output rank
+    # written once (value of the element's size + 4 B index), plus the offsets array when given.
+    out_bytes = 4 + (0 if flags & bt.INDICES_ONLY else elem_bytes)
+    alg_bytes = elem_bytes * n_elements + out_bytes * seg_num * k + (0 if offsets is None else 4 * (seg_num + 1))
     if args.op == "sample":
         alg_bytes += 8 * seg_num  # one uniform in, one sampled index out per row
     # The kernel's average launch duration over the timed region (back-to-back launches,
@@ -274,7 +285,7 @@ def main() -> int:
     step_us = ms_per_step * 1e3
     achieved = alg_bytes / (step_us * 1e-6)
     value = seg_num * steps / (total_ms * 1e-3)
-    dname = "fp16" if args.dtype == "f16" else "bf16"
+    dname = {"f16": "fp16", "bf16": "bf16", "f32": "fp32"}[args.dtype]
     metric = METRIC if (args.workload == "llm_logits" and k == 50 and args.dtype == "f16" and args.op == "topk"
                         and not flags) else \
         f"segments/s and achieved HBM GB/s, {dname} top-{k}{' sampling' if args.op == 'sample' else ''} " \
@@ -290,7 +301,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u16" if args.dtype == "f16" else "u16 (bf16 keys)",
+        "dtype": {"f16": "u16", "bf16": "u16 (bf16 keys)", "f32": "u32 (fp32 keys)"}[args.dtype],
         "data": "synthetic",
         "config": dict(cfg, k=k, input_copies=copies, parallelism="single GPU",
                        **({"output": args.output} if flags else {}),

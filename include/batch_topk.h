@@ -134,9 +134,31 @@ int radix_topk_sample_bf16(const uint16_t* d_logits, int seg_num, int seg_len, i
                            void* d_workspace, size_t workspace_bytes, void* stream);
 size_t radix_topk_sample_bf16_workspace_size(int seg_num, int seg_len, int k);
 
+/*
+ * fp32 twins of the four fixed-length and segmented entry points: the same arguments,
+ * contract and error behaviour, for float input and float output values (the raw 32-bit
+ * patterns of the selected elements, NaN payloads and the sign of zero preserved; pads are
+ * index -1 with bits 0xFFFFFFFF).  The order is the reference verifier's own, which compares
+ * floats (reference include/batch_topk_types.cuh:70-82): larger first, ties by ascending
+ * index, every NaN below -inf, +0 equal to -0.  Pointers must be 4-byte aligned.  Workspace
+ * sizes are their own (four elements per 16-byte load instead of eight); a segment needing
+ * more cooperative workgroups than an MI355X has CUs (k large and more than 16.7 M floats)
+ * is unsupported (size 0).  No counterpart in the reference, whose codec covers fp16 only.
+ */
+int radix_topk_batch_topk_f32(const float* d_input, int seg_num, int seg_len, int k,
+                              float* d_output_values, int32_t* d_output_indices,
+                              void* d_workspace, size_t workspace_bytes, void* stream);
+size_t radix_topk_batch_topk_f32_workspace_size(int seg_num, int seg_len, int k);
+int radix_topk_batch_topk_f32_segmented(const float* d_input, const int32_t* d_offsets,
+                                        int seg_num, int max_seg_len, int k,
+                                        float* d_output_values, int32_t* d_output_indices,
+                                        void* d_workspace, size_t workspace_bytes, void* stream);
+size_t radix_topk_batch_topk_f32_segmented_workspace_size(int seg_num, int max_seg_len, int k);
+
 /* Element formats and output flags of radix_topk_batch_topk_ex. */
 #define RADIX_TOPK_FORMAT_F16 0  /* IEEE binary16 bit patterns */
 #define RADIX_TOPK_FORMAT_BF16 1 /* bfloat16 bit patterns */
+#define RADIX_TOPK_FORMAT_F32 2  /* IEEE binary32 (float); values are 4 bytes */
 #define RADIX_TOPK_UNSORTED 1     /* each row's selected entries in unspecified order */
 #define RADIX_TOPK_INDICES_ONLY 2 /* no values: d_output_values may be NULL and is not written */
 

@@ -28,6 +28,9 @@
 //     bfloat16 -> float widening (the 16 bits become the float's high half), so the
 //     reference's comparator applies unchanged; its key (oracle_encode_bf16_desc) is the
 //     reference codec's pattern with bfloat16's inf/NaN boundary (0x7F80);
+//   * fp32 segments (oracle_batch_topk_f32): the verifier on the floats themselves, the
+//     reference comparator's own operand type; values are the raw 32-bit input patterns and
+//     pads are index -1 with bits 0xFFFFFFFF;
 //   * variable-length segments given by an int64 offset array;
 //   * ranks >= min(k, len) of a short segment are padded with index -1 and value bits 0xFFFF.
 
@@ -402,27 +405,13 @@ void oracle_histogram_pass(const uint16_t* input, int n, int shift, uint16_t pre
   }
 }
 
-// Batched verifier: for each segment, the reference's cpu_reference_topk on the exact
-// float widening of the fp16 input; values are written as the raw input bits at the
-// selected index.  offsets == nullptr selects fixed-length segments of seg_len.
-// threads <= 1 runs serially, exactly like the reference harness loop.
-static int batch_topk_16(const uint16_t* input, const int64_t* offsets, int seg_num,
-                         int64_t seg_len, int k, uint16_t* out_vals, int32_t* out_idx,
-                         int threads, ToFloat to_float) {
-  if (seg_num <= 0 || k <= 0) return 1;
-  auto run = [&](int s_begin, int s_end) {
-    std::vector<float> f;
-    std::vector<int> idx;
-    for (int s = s_begin; s < s_end; ++s) {
-      int64_t b, e;
-      segment_bounds(offsets, seg_len, s, &b, &e);
-      segment_topk_raw(input + b, e - b, k, out_vals + static_cast<int64_t>(s) * k,
-                       out_idx + static_cast<int64_t>(s) * k, f, idx, to_float);
-    }
-  };
+// Runs run(s_begin, s_end) over the segments, serially when threads <= 1 (exactly like the
+// reference harness loop), else split over `threads` host threads.
+extern "C++" template <class Run>
+void over_segments(int seg_num, int threads, Run run) {
   if (threads <= 1 || seg_num == 1) {
     run(0, seg_num);
-    return 0;
+    return;
   }
   const int nt = std::min(threads, seg_num);
   std::vector<std::thread> pool;
@@ -432,6 +421,58 @@ static int batch_topk_16(const uint16_t* input, const int64_t* offsets, int seg_
     pool.emplace_back(run, b, e);
   }
   for (auto& th : pool) th.join();
+}
+
+// Batched verifier: for each segment, the reference's cpu_reference_topk on the exact
+// float widening of the fp16 input; values are written as the raw input bits at the
+// selected index.  offsets == nullptr selects fixed-length segments of seg_len.
+static int batch_topk_16(const uint16_t* input, const int64_t* offsets, int seg_num,
+                         int64_t seg_len, int k, uint16_t* out_vals, int32_t* out_idx,
+                         int threads, ToFloat to_float) {
+  if (seg_num <= 0 || k <= 0) return 1;
+  over_segments(seg_num, threads, [&](int s_begin, int s_end) {
+    std::vector<float> f;
+    std::vector<int> idx;
+    for (int s = s_begin; s < s_end; ++s) {
+      int64_t b, e;
+      segment_bounds(offsets, seg_len, s, &b, &e);
+      segment_topk_raw(input + b, e - b, k, out_vals + static_cast<int64_t>(s) * k,
+                       out_idx + static_cast<int64_t>(s) * k, f, idx, to_float);
+    }
+  });
+  return 0;
+}
+
+// fp32 segments: cpu_reference_topk on the floats themselves (its comparator's own operand
+// type); values are the raw 32-bit input patterns at the selected index, pads index -1 with
+// bits 0xFFFFFFFF.
+int oracle_batch_topk_f32(const uint32_t* input, const int64_t* offsets, int seg_num,
+                          int64_t seg_len, int k, uint32_t* out_vals, int32_t* out_idx,
+                          int threads) {
+  if (seg_num <= 0 || k <= 0) return 1;
+  over_segments(seg_num, threads, [&](int s_begin, int s_end) {
+    std::vector<float> f;
+    std::vector<int> idx;
+    for (int s = s_begin; s < s_end; ++s) {
+      int64_t b, e;
+      segment_bounds(offsets, seg_len, s, &b, &e);
+      const int64_t len = e - b;
+      uint32_t* ov = out_vals + static_cast<int64_t>(s) * k;
+      int32_t* oi = out_idx + static_cast<int64_t>(s) * k;
+      int got = 0;
+      if (len > 0) {
+        f.resize(static_cast<size_t>(len));
+        std::memcpy(f.data(), input + b, static_cast<size_t>(len) * 4);
+        idx.resize(static_cast<size_t>(std::min<int64_t>(k, len)));
+        got = cpu_reference_topk(f.data(), static_cast<int>(len), static_cast<int>(len), k, nullptr,
+                                 idx.data());
+      }
+      for (int r = 0; r < k; ++r) {
+        oi[r] = r < got ? idx[static_cast<size_t>(r)] : -1;
+        ov[r] = r < got ? input[b + idx[static_cast<size_t>(r)]] : 0xffffffffu;
+      }
+    }
+  });
   return 0;
 }
 

@@ -28,6 +28,11 @@ How each oracle function is pinned (tests/test_oracle.py):
 * simulate_radix_boundary / select / finalize: the reference's state KATs
   (test/test_batch_topk.cu:66-74, 169-201, 203-234) and a brute-force cumulative count.
 * half <-> float conversions: numpy's float16 casts over every bit pattern.
+* fp32 (an extension): the verifier itself compares floats, so the batched fp32 oracle is
+  the reference's verifier on the input floats; it is checked against the numpy lexsort
+  restatement with the 32-bit key (``encode_f32_desc_np``) on random data with NaN payloads,
+  +-0, +-inf and subnormals, the key against float order on every special class and a
+  large random sample, and the reference's own host KATs (exact in fp32).
 * bfloat16 (an extension: the reference covers fp16 only): the bf16 -> float widening
   against torch's bfloat16 cast over every bit pattern; the bf16 key against float order
   over every bit pattern and hand-derived known answers; the batched bf16 verifier against
@@ -110,6 +115,9 @@ def lib():
         L.oracle_batch_topk_bf16.restype = ctypes.c_int
         L.oracle_batch_topk_bf16.argtypes = [vp, vp, ctypes.c_int, i64, ctypes.c_int, vp, vp,
                                              ctypes.c_int]
+        L.oracle_batch_topk_f32.restype = ctypes.c_int
+        L.oracle_batch_topk_f32.argtypes = [vp, vp, ctypes.c_int, i64, ctypes.c_int, vp, vp,
+                                            ctypes.c_int]
         L.oracle_batch_topk_half.restype = ctypes.c_int
         L.oracle_batch_topk_half.argtypes = [vp, vp, ctypes.c_int, i64, ctypes.c_int, vp, vp,
                                              ctypes.c_int]
@@ -216,10 +224,12 @@ def batch_topk_half(bits: np.ndarray, k: int, seg_len: int | None = None,
     """Reference order on every segment -> (values uint16 [S,k], indices int32 [S,k]).
 
     Values are the raw input bits at the selected index; ranks beyond a segment's length
-    are padded with (PAD_VALUE_BITS, PAD_INDEX).  ``fmt`` is "f16" (the reference's format)
-    or "bf16" (the same verifier on bfloat16 bits).
+    are padded with (PAD_VALUE_BITS, PAD_INDEX).  ``fmt`` is "f16" (the reference's format),
+    "bf16" (the same verifier on bfloat16 bits) or "f32" (the verifier on the floats
+    themselves: uint32 bits in, uint32 values out, pads 0xFFFFFFFF).
     """
-    bits = np.ascontiguousarray(bits, dtype=np.uint16).reshape(-1)
+    wide = fmt == "f32"
+    bits = np.ascontiguousarray(bits, dtype=np.uint32 if wide else np.uint16).reshape(-1)
     if offsets is not None:
         off = np.ascontiguousarray(offsets, dtype=np.int64)
         seg_num = off.size - 1
@@ -229,9 +239,10 @@ def batch_topk_half(bits: np.ndarray, k: int, seg_len: int | None = None,
         off = None
         seg_num = bits.size // seg_len
         sl = seg_len
-    vals = np.empty((seg_num, k), dtype=np.uint16)
+    vals = np.empty((seg_num, k), dtype=np.uint32 if wide else np.uint16)
     idx = np.empty((seg_num, k), dtype=np.int32)
-    fn = {"f16": lib().oracle_batch_topk_half, "bf16": lib().oracle_batch_topk_bf16}[fmt]
+    fn = {"f16": lib().oracle_batch_topk_half, "bf16": lib().oracle_batch_topk_bf16,
+          "f32": lib().oracle_batch_topk_f32}[fmt]
     rc = fn(_ptr(bits), _ptr(off) if off is not None else None, int(seg_num), int(sl), int(k),
             _ptr(vals), _ptr(idx), int(threads))
     if rc != 0:
@@ -286,17 +297,30 @@ def encode_bf16_desc_np(bits: np.ndarray) -> np.ndarray:
     return key.astype(np.uint16)
 
 
+def encode_f32_desc_np(bits: np.ndarray) -> np.ndarray:
+    """The same key for fp32 bits: NaN -> 0xFFFFFFFF, +-0 -> 0x7FFFFFFF, negative -> bits,
+    positive -> bits ^ 0x7FFFFFFF."""
+    b = np.asarray(bits, dtype=np.uint32).astype(np.uint64)
+    mag = b & 0x7FFFFFFF
+    key = np.where((b & 0x80000000) != 0, b, b ^ 0x7FFFFFFF)
+    key = np.where(mag == 0, 0x7FFFFFFF, key)
+    key = np.where(mag > 0x7F800000, 0xFFFFFFFF, key)
+    return key.astype(np.uint32)
+
+
 def topk_lexsort_np(bits: np.ndarray, k: int, seg_len: int | None = None,
                     offsets: np.ndarray | None = None, fmt: str = "f16"):
     """Independent numpy statement of the order: ascending (desc key, index)."""
-    encode = encode_half_desc_np if fmt == "f16" else encode_bf16_desc_np
-    bits = np.asarray(bits, dtype=np.uint16).reshape(-1)
+    encode = {"f16": encode_half_desc_np, "bf16": encode_bf16_desc_np, "f32": encode_f32_desc_np}[fmt]
+    wide = fmt == "f32"
+    bits = np.asarray(bits, dtype=np.uint32 if wide else np.uint16).reshape(-1)
     if offsets is None:
         seg_num = bits.size // seg_len
         offsets = np.arange(seg_num + 1, dtype=np.int64) * seg_len
     offsets = np.asarray(offsets, dtype=np.int64)
     seg_num = offsets.size - 1
-    vals = np.full((seg_num, k), PAD_VALUE_BITS, dtype=np.uint16)
+    vals = np.full((seg_num, k), 0xFFFFFFFF if wide else PAD_VALUE_BITS,
+                   dtype=np.uint32 if wide else np.uint16)
     idx = np.full((seg_num, k), PAD_INDEX, dtype=np.int32)
     for s in range(seg_num):
         seg = bits[offsets[s]:offsets[s + 1]]

@@ -125,7 +125,9 @@ def test_kernel_resources_keep_occupancy_without_spills():
 
     usage = resource_usage()
     kernels = {k: v for k, v in usage.items() if "segmented_topk_kernel" in k}
-    assert len(kernels) == 13, sorted(kernels)
+    # 12 workgroup shapes + the cooperative one, each for 16-bit and for 32-bit elements
+    assert len(kernels) == 26, sorted(kernels)
+    assert sum("Elem32" in k for k in kernels) == 13, sorted(kernels)
     for name, r in kernels.items():
         assert r["ScratchSize [bytes/lane]"] == 0, (name, r)
         assert r["Occupancy [waves/SIMD]"] >= 4, (name, r)
@@ -148,13 +150,43 @@ def test_sample_validation_rejects_before_any_hip_call():
             assert fn(**dict(ok, **bad)) == INVALID, (fn.__name__, bad)
 
 
+def test_f32_entry_points_validate_and_size():
+    # fp32 rows are planned with four elements per 16-byte load: their own workspace sizes
+    assert bt.batch_topk_f32_workspace_size(128, 128256, 50) > 1
+    assert bt.batch_topk_f32_workspace_size(1, 10, 11) == 0
+    assert bt.batch_topk_f32_workspace_size(0, 10, 1) == 0
+    assert bt.batch_topk_f32_segmented_workspace_size(4, 1000, 64) > 1
+    assert bt.batch_topk_ex_workspace_size(bt.FORMAT_F32, False, 128, 128256, 50) == \
+        bt.batch_topk_f32_workspace_size(128, 128256, 50)
+    assert bt.batch_topk_ex_workspace_size(bt.FORMAT_F32, True, 4, 1000, 64) == \
+        bt.batch_topk_f32_segmented_workspace_size(4, 1000, 64)
+    # a cooperative grid beyond 256 workgroups is unsupported: 2^24 floats with k = 1024 take
+    # 256 chunks when 16-byte aligned (a misaligned pointer is refused at launch); two such
+    # rows take 512
+    assert bt.batch_topk_f32_workspace_size(1, 1 << 24, 1024) > 1
+    assert bt.batch_topk_f32_workspace_size(2, 1 << 24, 1024) == 0
+    assert bt.batch_topk_f32_workspace_size(1, (1 << 24) + 1, 1024) == 0
+    ws = bt.batch_topk_f32_workspace_size(1, 10000, 50)
+    call = bt.batch_topk_f32
+    assert call(0, 1, 10000, 50, P_VAL, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, 1, 10000, 50, 0, P_IDX, P_WS, ws) == INVALID
+    assert call(P_IN, 1, 10, 11, P_VAL, P_IDX, P_WS, 1 << 20) == INVALID
+    assert call(P_IN, 1, 10000, 50, P_VAL, P_IDX, P_WS, ws - 1) == INVALID
+    assert call(P_IN + 2, 1, 10000, 50, P_VAL, P_IDX, P_WS, ws) == INVALID   # floats: 4-byte aligned
+    assert call(P_IN, 1, 10000, 50, P_VAL + 2, P_IDX, P_WS, ws) == INVALID
+    seg = bt.batch_topk_f32_segmented
+    wss = bt.batch_topk_f32_segmented_workspace_size(4, 1000, 64)
+    assert seg(P_IN, 0, 4, 1000, 64, P_VAL, P_IDX, P_WS, wss) == INVALID
+    assert seg(P_IN + 2, P_OFF, 4, 1000, 64, P_VAL, P_IDX, P_WS, wss) == INVALID
+
+
 def test_ex_workspace_matches_the_plain_entry_points():
     for fmt in (bt.FORMAT_F16, bt.FORMAT_BF16):
         for shape in ((1, 10000, 50), (128, 128256, 50), (3, 250000, 512), (1, 16777216, 1024)):
             assert bt.batch_topk_ex_workspace_size(fmt, False, *shape) == bt.batch_topk_half_workspace_size(*shape)
             assert bt.batch_topk_ex_workspace_size(fmt, True, *shape) == \
                 bt.batch_topk_half_segmented_workspace_size(*shape)
-    assert bt.batch_topk_ex_workspace_size(2, False, 1, 10000, 50) == 0   # unknown format
+    assert bt.batch_topk_ex_workspace_size(3, False, 1, 10000, 50) == 0   # unknown format
     assert bt.batch_topk_ex_workspace_size(bt.FORMAT_F16, False, 1, 10, 11) == 0
     assert bt.batch_topk_ex_workspace_size(bt.FORMAT_F16, True, 1, 10, 11) > 1  # short segments pad
 
@@ -163,7 +195,7 @@ def test_ex_validation_rejects_before_any_hip_call():
     ws = bt.batch_topk_ex_workspace_size(bt.FORMAT_F16, True, 4, 1000, 64)
     ok = dict(d_input=P_IN, fmt=bt.FORMAT_F16, d_offsets=P_OFF, seg_num=4, seg_len=1000, k=64, flags=0,
               d_output_values=P_VAL, d_output_indices=P_IDX, d_workspace=P_WS, workspace_bytes=ws)
-    for bad in (dict(fmt=2), dict(fmt=-1), dict(flags=4), dict(flags=-1),
+    for bad in (dict(fmt=3), dict(fmt=-1), dict(flags=4), dict(flags=-1),
                 dict(d_output_values=0), dict(d_output_values=0, flags=bt.UNSORTED),
                 dict(d_input=0), dict(d_output_indices=0), dict(d_workspace=0),
                 dict(seg_num=0), dict(seg_len=-1), dict(k=0), dict(k=bt.MAX_K + 1),

@@ -276,6 +276,95 @@ def test_bf16_brute_force_small_rows():
                 assert idx[0].tolist() == [rank.index(r) for r in range(k)]
 
 
+# ------------------------------------------------------------------ fp32 (extension)
+
+F32_SPECIALS = np.array([0x7FC00000, 0xFFC00001, 0x7F800001, 0x7FFFFFFF,   # NaNs, both signs
+                         0x00000000, 0x80000000, 0x7F800000, 0xFF800000,   # +0, -0, +inf, -inf
+                         0x00000001, 0x80000001, 0x007FFFFF, 0x3F800000,   # subnormals, 1.0
+                         0xBF800000, 0x3F800001], dtype=np.uint32)
+
+
+def _f32_bits(values):
+    return np.asarray(values, dtype=np.float32).view(np.uint32)
+
+
+def test_f32_reference_host_kats():
+    # test/test_batch_topk.cu:19-44, exact in fp32, through the batched fp32 verifier
+    v, i = O.batch_topk_half(_f32_bits([5, 7, 7, 1]), 2, seg_len=4, fmt="f32")
+    assert i[0].tolist() == [1, 2] and v[0].view(np.float32).tolist() == [7, 7]
+    v, i = O.batch_topk_half(_f32_bits([np.nan, 3, -1, np.nan]), 3, seg_len=4, fmt="f32")
+    assert i[0].tolist() == [1, 2, 0] and v[0][2] == _f32_bits([np.nan])[0]
+    v, i = O.batch_topk_half(_f32_bits([2, 1]), 4, offsets=np.array([0, 2]), fmt="f32")
+    assert i[0].tolist() == [0, 1, -1, -1] and v[0].tolist()[2:] == [0xFFFFFFFF] * 2
+
+
+def test_f32_key_orders_like_floats():
+    # the 32-bit key against float order: every special class and a random sample of patterns
+    rng = np.random.default_rng(3)
+    bits = np.concatenate([F32_SPECIALS, rng.integers(0, 2**32, size=200000, dtype=np.uint64).astype(np.uint32)])
+    keys = O.encode_f32_desc_np(bits).astype(np.int64)
+    with np.errstate(invalid="ignore"):
+        f = bits.view(np.float32).astype(np.float64)
+    nan = np.isnan(f)
+    assert np.all(keys[nan] == 0xFFFFFFFF) and np.all(keys[~nan] < 0xFFFFFFFF)
+    g = f[~nan]
+    kg = keys[~nan]
+    order = np.argsort(kg, kind="stable")
+    assert np.all(np.diff(g[order]) <= 0)                     # ascending key = descending value
+    eq = np.diff(kg[order]) == 0
+    assert np.all(np.diff(g[order])[eq] == 0)                  # equal keys only for equal values
+    assert np.all(np.diff(g[order])[~eq] < 0)                  # distinct values, distinct keys
+    assert O.encode_f32_desc_np(np.array([0x00000000, 0x80000000], dtype=np.uint32)).tolist() == [0x7FFFFFFF] * 2
+
+
+def test_f32_verifier_matches_numpy_lexsort_with_specials():
+    rng = np.random.default_rng(11)
+    seg_len = 3001
+    bits = rng.standard_normal(40 * seg_len).astype(np.float32).view(np.uint32).copy()
+    pos = rng.integers(0, bits.size, size=bits.size // 8)
+    bits[pos] = F32_SPECIALS[rng.integers(0, F32_SPECIALS.size, size=pos.size)]
+    bits[rng.integers(0, bits.size, size=bits.size // 8)] = _f32_bits([1.5])[0]   # ties
+    for k in (1, 7, 50, 300):
+        got = O.batch_topk_half(bits, k, seg_len=seg_len, fmt="f32", threads=4)
+        exp = O.topk_lexsort_np(bits, k, seg_len=seg_len, fmt="f32")
+        assert np.array_equal(got[0], exp[0]) and np.array_equal(got[1], exp[1]), k
+
+
+def test_f32_verifier_agrees_with_fp16_on_widened_rows():
+    # fp16 values widen exactly to fp32 and keep their order: the fp32 verifier must select
+    # what the (pinned) fp16 verifier selects, with the widened values
+    rng = np.random.default_rng(12)
+    h = rng.integers(0, 65536, size=30 * 2000).astype(np.uint16)
+    f = h.view(np.float16).astype(np.float32)
+    for k in (1, 64, 500):
+        v16, i16 = O.batch_topk_half(h, k, seg_len=2000)
+        v32, i32 = O.batch_topk_half(f.view(np.uint32), k, seg_len=2000, fmt="f32")
+        assert np.array_equal(i16, i32), k
+        ok = i16 >= 0
+        w = v16.view(np.float16).astype(np.float32).view(np.uint32)
+        nan = np.isnan(v16.view(np.float16))
+        assert np.array_equal(w[ok & ~nan], v32[ok & ~nan]), k   # NaN payloads widen differently
+
+
+def test_f32_brute_force_small_rows():
+    alpha = F32_SPECIALS[[0, 1, 4, 5, 6, 7, 8, 11]]
+    for n in range(1, 4):
+        for row in itertools.product(range(len(alpha)), repeat=n):
+            bits = alpha[list(row)]
+            f = bits.view(np.float32)
+            def beats(j, i):
+                if np.isnan(f[j]) != np.isnan(f[i]):
+                    return np.isnan(f[i])
+                if not np.isnan(f[j]) and f[j] != f[i]:
+                    return f[j] > f[i]
+                return j < i
+            rank = [sum(1 for j in range(n) if beats(j, i)) for i in range(n)]
+            for k in range(1, n + 1):
+                v, idx = O.batch_topk_half(bits, k, seg_len=n, fmt="f32")
+                assert idx[0].tolist() == [rank.index(r) for r in range(k)]
+                assert v[0].tolist() == [int(bits[rank.index(r)]) for r in range(k)]
+
+
 # ------------------------------------------------------------------ sampling consumer
 
 def test_sample_rule_matches_scipy_softmax():
