@@ -1,7 +1,9 @@
-// Fused segmented fp16 top-k for gfx950 (MI355X).
+// Fused segmented top-k for gfx950 (MI355X): fp16 and bf16 (16-bit elements) and fp32.
 //
-// One workgroup owns one chunk (block * vpt * 8 elements) of one segment; a segment of up to
-// 131,072 elements is a single chunk.  The chunk is read from HBM exactly once, with
+// One workgroup owns one chunk (block * vpt * 8 16-bit elements, or * 4 floats) of one
+// segment; a segment of up to 131,072 16-bit elements is a single chunk.  The steps below are
+// written for 16-bit elements; for fp32 they run on the top 16 bits of the 32-bit key, and
+// the candidates carry the exact key (see Elem16 / Elem32).  The chunk is read from HBM exactly once, with
 // nontemporal 16-byte loads that are all issued up front, into registers.  Everything after
 // the load runs on registers and LDS, overlapped with the loads still in flight:
 //
