@@ -22,8 +22,8 @@
       fp16 batch, rotating over 17 input copies (557 MB), for several workgroup shapes.
 
   python -m batch_topk_amd.profiling matrix [--out FILE]
-      bench.py over every workload (fp16, plus bf16 and the sampling consumer on the LLM
-      logits), as a markdown table.
+      bench.py over every workload (fp16; bf16 and the sampling consumer on the LLM logits;
+      fp32 on every workload; the unsorted and indices-only outputs), as a markdown table.
 """
 
 from __future__ import annotations
@@ -134,6 +134,16 @@ MATRIX = (
     ("huge_segment", ["--k", "1024"]),
     ("llm_logits", ["--k", "50", "--dtype", "bf16"]),
     ("llm_logits", ["--k", "50", "--op", "sample"]),
+    ("llm_logits", ["--k", "50", "--dtype", "f32"]),
+    ("uniform_small", ["--k", "50", "--dtype", "f32"]),
+    ("varlen", ["--k", "64", "--dtype", "f32"]),
+    ("ties_special", ["--k", "16", "--dtype", "f32"]),
+    ("ties_special", ["--k", "256", "--dtype", "f32"]),
+    ("huge_segment", ["--k", "1024", "--dtype", "f32"]),
+    ("ties_special", ["--k", "128", "--output", "unsorted"]),
+    ("ties_special", ["--k", "256", "--output", "unsorted"]),
+    ("varlen", ["--k", "64", "--output", "unsorted"]),
+    ("llm_logits", ["--k", "50", "--output", "indices"]),
 ) + tuple(("ref_matrix", ["--k", "50", "--seg-num", str(n), "--no-cpu-baseline"])
           for n in (128, 1500, 3000, 4500, 6000))
 

@@ -312,7 +312,7 @@ def main() -> int:
             "peak": HBM_PEAK_BPS / 1e9,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_BPS,
-            "traffic": load_traffic(args.workload if args.dtype == "f16" else f"{args.workload}:bf16", k)
+            "traffic": load_traffic(args.workload if args.dtype == "f16" else f"{args.workload}:{args.dtype}", k)
             if args.op == "topk" and not flags else None,
         },
         "elements_per_s": n_elements * steps / (total_ms * 1e-3),
