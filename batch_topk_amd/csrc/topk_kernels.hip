@@ -672,7 +672,8 @@ __device__ __forceinline__ void group_barrier(u64* slots, u64 epoch, int w, int 
 template <int BLOCK>
 __device__ void group_histogram(u32* lds_hist, u32* ghist, u32* scratch, u64* slots, u64 epoch, int w,
                                 int arrivals) {
-  static_assert(BLOCK == 1024, "the copy sum assumes 4 threads per bin");
+  constexpr int Q = BLOCK / 256;  // threads per bin in the copy sum
+  static_assert(Q >= 1 && kGroupCopies % Q == 0, "the copy sum splits the copies over Q threads per bin");
   const int tid = threadIdx.x;
   if (tid < 256) {
     const u32 c = lds_hist[tid];
@@ -686,10 +687,15 @@ __device__ void group_histogram(u32* lds_hist, u32* ghist, u32* scratch, u64* sl
   const int q = tid >> 8;
   u32 part = 0;
 #pragma unroll
-  for (int c = 0; c < kGroupCopies / 4; ++c) part += load_agent(ghist + (q + 4 * c) * 256 + bin);
+  for (int c = 0; c < kGroupCopies / Q; ++c) part += load_agent(ghist + (q + Q * c) * 256 + bin);
   scratch[q * 256 + bin] = part;
   __syncthreads();
-  if (tid < 256) lds_hist[tid] = scratch[tid] + scratch[256 + tid] + scratch[512 + tid] + scratch[768 + tid];
+  if (tid < 256) {
+    u32 sum = 0;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) sum += scratch[i * 256 + tid];
+    lds_hist[tid] = sum;
+  }
   __syncthreads();
 }
 
@@ -1188,6 +1194,10 @@ segmented_topk_kernel(TopkParams p) {
     const u32 traw = T == 0x7fffu ? 0x8000u : T;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
+      // the wave's positions of vector j: skip the whole vector (wave-uniform) when none
+      // is in [lo, hi), as in every vector of a short segment past its end
+      const int wpos = (j * BLOCK + wid * 64) * EV;
+      if (wpos >= hi || wpos + 64 * EV <= lo) continue;
       const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
       for (int e = 0; e < EV; ++e) {
@@ -1333,9 +1343,12 @@ segmented_topk_kernel(TopkParams p) {
     return;
   }
   if (all_mode && nc <= kArea) {
-    // Every in-range element, at its position: no counting needed.
+    // Every in-range element, at its position: no counting needed.  Vectors whose wave range
+    // holds no position of [lo, hi) are skipped as a whole (wave-uniform).
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
+      const int wpos = (j * BLOCK + wid * 64) * EV;
+      if (wpos >= hi || wpos + 64 * EV <= lo) continue;
       const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
       for (int e = 0; e < EV; ++e) {
