@@ -831,7 +831,7 @@ __device__ __forceinline__ u32 vec_min2(const uint4& x) {
 
 // At least 4 waves per SIMD (at most 128 VGPRs): one 1024-thread workgroup, or two 512-thread
 // ones, per CU.  (Fewer, fatter waves -- 512 threads x 32 vectors -- measured slower.)
-template <int BLOCK, int VPT, bool COOP, class E>
+template <int BLOCK, int VPT, bool COOP, class E, bool SHORT = false>
 __global__ void __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4)))
 segmented_topk_kernel(TopkParams p) {
   constexpr int NW = BLOCK / 64;
@@ -1022,7 +1022,26 @@ segmented_topk_kernel(TopkParams p) {
   // summed over the segment's workgroups in one meeting; T is the last key of the fine bin
   // holding the kk-th best, so at least kk real elements are at or below it, and at most that
   // bin's other keys' worth of extra elements pass.
-  atomicAdd(&sm.hist[best_key >> 8], 1u);
+  //   A short chunk (every position in each thread's first vector, at most 4 * EV * kc of
+  // them) ranks its elements instead of its thread bests: then few threads hold a real best,
+  // and a thread-best threshold would let most of the chunk through.  At most EV LDS atomics
+  // per thread, and T is the chunk's exact kc-th key prefix.  Compiled only into the SHORT
+  // instantiations, which the launch picks when a chunk can be short (segmented input, or
+  // rows this short): elsewhere the unused branch measurably slows the threshold step.
+  constexpr bool kElemMode = !COOP && SHORT;
+  const bool elem_mode = kElemMode && hi <= BLOCK * EV && nc <= 4 * EV * kc;  // workgroup-uniform
+  u32 ekeys[EV];  // key prefixes of this thread's first vector (elem_mode), 0x10000 if outside
+  if (__builtin_expect(elem_mode, 0)) {
+    const u32 w4[4] = {v[0].x, v[0].y, v[0].z, v[0].w};
+#pragma unroll
+    for (int e = 0; e < EV; ++e) {
+      const int pos = tid * EV + e;
+      ekeys[e] = (pos >= lo && pos < hi) ? E::prefix(E::element(w4, e), inf) : 0x10000u;
+      if (ekeys[e] < 0x10000u) atomicAdd(&sm.hist[ekeys[e] >> 8], 1u);
+    }
+  } else {
+    atomicAdd(&sm.hist[best_key >> 8], 1u);
+  }
   if (tid < 256) sm.hist2[tid] = 0;
   if (tid == 0) sm.scal[4] = 0;  // candidate list counter
   u32 T;
@@ -1076,7 +1095,14 @@ segmented_topk_kernel(TopkParams p) {
     __syncthreads();
     TOPK_TRACE(2);
     const u32 b1 = static_cast<u32>(sm.scal[8]);
-    if ((best_key >> 8) == b1) atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
+    if (__builtin_expect(elem_mode, 0)) {
+#pragma unroll
+      for (int e = 0; e < EV; ++e) {
+        if ((ekeys[e] >> 8) == b1) atomicAdd(&sm.hist2[ekeys[e] & 0xffu], 1u);
+      }
+    } else if ((best_key >> 8) == b1) {
+      atomicAdd(&sm.hist2[best_key & 0xffu], 1u);
+    }
     __syncthreads();
     if (wid == 0) wave_find_bucket(sm.hist2, need - sm.scal[9], sm.scal + 12, lane);
     __syncthreads();
@@ -1524,6 +1550,16 @@ segmented_topk_kernel(TopkParams p) {
 template <int BLOCK, int VPT, class E>
 int launch_shape(const Plan& plan, const TopkParams& params, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(params.seg_num) * params.chunks_per_seg));
+  // Chunks that can be short (all positions in each thread's first vector, at most 4 * EV * k
+  // elements): segmented input, or fixed-length rows that short.
+  const int64_t ev = E::kPerVec;
+  const bool short_chunks = params.offsets != nullptr ||
+                            (params.seg_len + ev - 1 <= BLOCK * ev && params.seg_len <= 4 * ev * params.k);
+  if (short_chunks) {
+    hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT, false, E, true>), grid, dim3(BLOCK),
+                       static_cast<unsigned>(plan.lds_bytes), stream, params);
+    return static_cast<int>(hipGetLastError());
+  }
   hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT, false, E>), grid, dim3(BLOCK),
                      static_cast<unsigned>(plan.lds_bytes), stream, params);
   return static_cast<int>(hipGetLastError());

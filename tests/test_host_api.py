@@ -125,9 +125,10 @@ def test_kernel_resources_keep_occupancy_without_spills():
 
     usage = resource_usage()
     kernels = {k: v for k, v in usage.items() if "segmented_topk_kernel" in k}
-    # 12 workgroup shapes + the cooperative one, each for 16-bit and for 32-bit elements
-    assert len(kernels) == 26, sorted(kernels)
-    assert sum("Elem32" in k for k in kernels) == 13, sorted(kernels)
+    # 12 workgroup shapes + the cooperative one, plus the 12 shapes again with the short-chunk
+    # threshold, each for 16-bit and for 32-bit elements
+    assert len(kernels) == 50, sorted(kernels)
+    assert sum("Elem32" in k for k in kernels) == 25, sorted(kernels)
     for name, r in kernels.items():
         assert r["ScratchSize [bytes/lane]"] == 0, (name, r)
         assert r["Occupancy [waves/SIMD]"] >= 4, (name, r)
