@@ -276,15 +276,21 @@ __device__ __forceinline__ void wave_find_bucket(const u32* hist, int need, int*
 
 // Exact radix select over M unique packed values in LDS: returns the bound B such that
 // exactly kk values are <= B (1 <= kk <= M).  8-bit digits over the key and index fields,
-// MSB first, early exit as soon as a bucket is taken whole.
+// MSB first, early exit as soon as a bucket is taken whole.  Indices are below n, so the index
+// bytes above n - 1's highest byte are zero in every entry and take no pass.
 template <int BLOCK, class E>
-__device__ u64 block_select_bound(const u64* list, int M, int kk, u32* hist, int* scal) {
+__device__ u64 block_select_bound(const u64* list, int M, int kk, u32* hist, int* scal, int64_t n) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = tid >> 6;
+  const int idx_bytes = n <= 0x100 ? 1 : (n <= 0x10000 ? 2 : (n <= 0x1000000 ? 3 : 4));
   u64 prefix = 0, pmask = 0;
   int need = kk;
   for (int shift = 56; shift >= E::kLowDigit; shift -= 8) {
+    if (shift < E::kIdxShift + 32 && (shift - E::kIdxShift) / 8 >= idx_bytes) {
+      pmask |= 0xffull << shift;  // a zero index byte in every entry: digit 0, no pass
+      continue;
+    }
     for (int i = tid; i < 256; i += BLOCK) hist[i] = 0;
     __syncthreads();
     for (int i = tid; i < M; i += BLOCK) {
@@ -493,7 +499,7 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
   } else if (p.unsorted && !sampling) {
     // Unsorted output: the kk best, found by radix select, in the order they are found.
     if (M > kk) {
-      const u64 bound = block_select_bound<BLOCK, E>(sm.area, M, kk, sm.hist, sm.scal);
+      const u64 bound = block_select_bound<BLOCK, E>(sm.area, M, kk, sm.hist, sm.scal, n);
       if (tid == 0) sm.scal[3] = 0;
       __syncthreads();
       for (int i = tid; i < M; i += BLOCK) {
@@ -504,13 +510,14 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
       for (int i = tid; i < M; i += BLOCK) write_rank<E>(p, n, seg, i, sm.area[i]);
     }
   } else if (NW >= 8 && M <= 8 * NW * 4 && M <= 512) {
-    // Up to 512: every wave ranks its share against the whole list held in registers (a
-    // radix select first costs more: tied keys take it through the index digits).
+    // Up to 512: every wave ranks its share against the whole list held in registers (a radix
+    // select first, then ranking only kk, was measured no faster: tied keys take the select
+    // through the index digits, and the extra ranking code slows the other paths).
     if constexpr (NW >= 8) wave_rank_write<BLOCK, 8, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
   } else {
     const u64* sel = sm.area;
     if (M > kk) {
-      const u64 bound = block_select_bound<BLOCK, E>(sm.area, M, kk, sm.hist, sm.scal);
+      const u64 bound = block_select_bound<BLOCK, E>(sm.area, M, kk, sm.hist, sm.scal, n);
       if (tid == 0) sm.scal[3] = 0;
       __syncthreads();
       for (int i = tid; i < M; i += BLOCK) {
@@ -1436,7 +1443,7 @@ segmented_topk_kernel(TopkParams p) {
     const u64* src = sm.area;
     int M = C;
     if (C > p.cap_list) {
-      const u64 bound = block_select_bound<BLOCK, E>(sm.area, C, kc, sm.hist, sm.scal);
+      const u64 bound = block_select_bound<BLOCK, E>(sm.area, C, kc, sm.hist, sm.scal, n);
       if (tid == 0) sm.scal[3] = 0;
       __syncthreads();
       for (int i = tid; i < C; i += BLOCK) {
