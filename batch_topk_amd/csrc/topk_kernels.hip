@@ -822,9 +822,8 @@ __device__ __forceinline__ int vec_min4_i32(const uint4& x) {
   const int b = static_cast<int>(x.z) < static_cast<int>(x.w) ? static_cast<int>(x.z) : static_cast<int>(x.w);
   return a < b ? a : b;
 }
-// Largest int value of a per-vector max (either half of a packed pair, or the int32 itself).
+// Larger half of a packed int16 pair.
 __device__ __forceinline__ int vec_gmax(short2_t g) { return g.x > g.y ? g.x : g.y; }
-__device__ __forceinline__ int vec_gmax(int g) { return g; }
 __device__ __forceinline__ u32 vec_max2(const uint4& x) {
   return as_u32(__builtin_elementwise_max(__builtin_elementwise_max(as_s2(x.x), as_s2(x.y)),
                                           __builtin_elementwise_max(as_s2(x.z), as_s2(x.w))));
@@ -983,16 +982,17 @@ segmented_topk_kernel(TopkParams p) {
   // the thread's best unless it has none: then its best is the min (the negative value
   // nearest zero), and only a wave holding such a lane builds the min tree.  Every VALU
   // instruction here costs all 4 waves of the SIMD.
-  using VecMax = std::conditional_t<E::kBytes == 2, short2_t, int>;
-  VecMax gv[VPT];  // per-vector max, kept for the filter's vector test
+  // Per-vector max as one int, kept for the filter's vector test: reducing it here, while
+  // later waves' data is still in flight, leaves the filter one compare per vector.
+  int gv[VPT];
   int m1, m2;
   if constexpr (E::kBytes == 2) {
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) gv[j] = as_s2(vec_max2(v[j]));
-    short2_t mx = gv[0];
+    for (int j = 0; j < VPT; ++j) gv[j] = vec_gmax(as_s2(vec_max2(v[j])));
+    int mx = gv[0];
 #pragma unroll
-    for (int j = 1; j < VPT; ++j) mx = __builtin_elementwise_max(mx, gv[j]);
-    m1 = mx.x > mx.y ? mx.x : mx.y;  // int16 max: the best non-negative-sign half
+    for (int j = 1; j < VPT; ++j) mx = mx > gv[j] ? mx : gv[j];
+    m1 = mx;  // int16 max: the best non-negative-sign half
     m2 = 32767;
     if (ballot(m1 < 0)) {
       short2_t mn = as_s2(vec_min2(v[0]));
@@ -1168,24 +1168,35 @@ segmented_topk_kernel(TopkParams p) {
           }
         }
       }
-      const u32 cnt = static_cast<u32>(__builtin_popcount(hm));
-      const u32 incl = wave_inclusive_scan(cnt);
-      const u32 total = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
-      if (total) {
+      // List offsets: with at most one hit per lane (the usual case) a lane's offset is its
+      // rank among the hit lanes; otherwise a wave prefix sum of the hit counts.
+      const u64 hit_lanes = ballot(hm != 0u);
+      if (hit_lanes) {
+        u32 excl, total;
+        if (ballot((hm & (hm - 1u)) != 0u) == 0) {
+          excl = mbcnt(hit_lanes);
+          total = static_cast<u32>(__popcll(hit_lanes));
+        } else {
+          const u32 cnt = static_cast<u32>(__builtin_popcount(hm));
+          const u32 incl = wave_inclusive_scan(cnt);
+          total = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
+          excl = incl - cnt;
+        }
         u32 base = 0;
         if (lane == 0) base = atomicAdd(reinterpret_cast<u32*>(&sm.scal[4]), total);
-        u32 o = __builtin_amdgcn_readfirstlane(base) + incl - cnt;
+        u32 o = __builtin_amdgcn_readfirstlane(base) + excl;
         while (hm) {
           const u32 e = static_cast<u32>(__builtin_ctz(hm));
           hm &= hm - 1u;
           const u32 pi = p0 + e;
+          // the hit element, read back from the staged vector (cheaper than selecting it
+          // from the registers by a lane-varying index)
           if constexpr (E::kBytes == 2) {
-            const u32 word = e < 2u ? w4[0] : (e < 4u ? w4[1] : (e < 6u ? w4[2] : w4[3]));
-            const u32 b = (word >> ((e & 1u) * 16u)) & 0xffffu;
+            const u32 b = reinterpret_cast<const uint16_t*>(st_vec + lane)[e];
             if (o < static_cast<u32>(kArea))
               sm.area[o] = (static_cast<u64>(((b ^ 0x7fffu) << 16) | (pi >> 16)) << 32) | ((pi << 16) | b);
           } else {
-            const u32 b = e == 0u ? w4[0] : (e == 1u ? w4[1] : (e == 2u ? w4[2] : w4[3]));
+            const u32 b = reinterpret_cast<const u32*>(st_vec + lane)[e];
             if (o < static_cast<u32>(kArea)) sm.area[o] = (static_cast<u64>(b ^ 0x7fffffffu) << 32) | pi;
           }
           ++o;
@@ -1197,7 +1208,7 @@ segmented_topk_kernel(TopkParams p) {
     // Stage the passing vectors: one compare and ballot per vector gives the wave's passing
     // lanes, and a wave-uniform branch skips the vectors no lane passes.
     auto stage_vector = [&](int j) {  // inlined into unrolled loops: j is a constant
-      const bool mine = vec_gmax(gv[j]) >= static_cast<int>(t_lo);
+      const bool mine = gv[j] >= static_cast<int>(t_lo);
       const u64 m = ballot(mine);
       if (m) {
         const u32 c = static_cast<u32>(__popcll(m));
