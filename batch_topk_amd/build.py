@@ -21,6 +21,9 @@ SOURCES = ["topk_kernels.hip", "sample_kernels.hip", "api.cpp"]
 # batch_topk_amd/profiling.py only.
 FLOOR_LIB_PATH = os.path.join(HERE, "libread_floor.so")
 FLOOR_SOURCES = ["read_floor.hip"]
+# Measurement build of the engine with the per-phase clock stamps compiled in
+# (-DTOPK_PHASE_TRACE): loaded by batch_topk_amd/profiling.py only, never by the package.
+TRACE_LIB_PATH = os.path.join(HERE, "libbatch_topk_amd_trace.so")
 
 # -packed-fp32-ops: no v_pk_*_f32 in any code object (this engine has no fp32 math anyway).
 HIP_FLAGS = [
@@ -37,9 +40,9 @@ def hipcc() -> str:
     return path
 
 
-def _compile(sources, out_path: str, verbose: bool) -> None:
+def _compile(sources, out_path: str, verbose: bool, defines=()) -> None:
     tmp = out_path + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, "-shared", "-o", tmp,
+    cmd = [hipcc(), *HIP_FLAGS, *[f"-D{d}" for d in defines], "-shared", "-o", tmp,
            *[os.path.join(CSRC, s) for s in sources], "-lamdhip64"]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -52,9 +55,10 @@ def _compile(sources, out_path: str, verbose: bool) -> None:
 
 def build(verbose: bool = False) -> str:
     """Always recompiles (the build check must exercise the compiler): the engine library and
-    the read-floor measurement library."""
+    the two measurement libraries (read floor, phase-traced engine)."""
     _compile(SOURCES, LIB_PATH, verbose)
     _compile(FLOOR_SOURCES, FLOOR_LIB_PATH, verbose)
+    _compile(SOURCES, TRACE_LIB_PATH, verbose, defines=("TOPK_PHASE_TRACE",))
     return LIB_PATH
 
 

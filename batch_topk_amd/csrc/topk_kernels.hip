@@ -55,14 +55,50 @@
 #include "sample_row.hpp"
 #include "topk_common.hpp"
 
-// Phase timestamp hook for profiling builds; compiled out otherwise.
-#ifndef TOPK_TRACE
+// Phase timestamps, compiled only into the profiling build (-DTOPK_PHASE_TRACE, a library of
+// its own that batch_topk_amd.profiling loads); in the engine every hook is empty.
+//   TOPK_TRACE(id): thread 0 of workgroup b stores the shader clock (s_memtime) and the
+//     constant 100 MHz clock (s_memrealtime) in slot id of row b; id 0 also clears the row.
+//   TOPK_WTRACE(id): lane 0 of every wave stores the shader clock in slot id of its wave's row.
+//   TOPK_TRACE_VALUE(id, v): thread 0 stores v in slot id of row b (shader-clock table).
+// Slots: 0 start, 12 loads issued, 1 thread best, 2 first histogram round, 4 threshold,
+// 5 filter, 6 refinement done, 8 first meeting (cooperative) or list published (two-chunk
+// segment), 9 cooperative threshold, 10 list stored or lists merged, 3 cooperative lengths
+// read, 7 cooperative lists gathered, 11 end; values: 13 merger's poll rounds, 14 candidates,
+// 15 threshold.  Wave slots: 1 thread best, 0 threshold read, 2 filter start, 3 vectors
+// staged, 4 flushed, 5 after the filter barrier, 6 ranking start, 7 ranking end.
+#ifdef TOPK_PHASE_TRACE
+namespace radix_topk_amd_trace {
+constexpr int kMaxWorkgroups = 2048;
+__device__ unsigned long long g_clock[kMaxWorkgroups * 16];
+__device__ unsigned long long g_real[kMaxWorkgroups * 16];
+__device__ unsigned long long g_wave[kMaxWorkgroups * 16 * 16];
+}  // namespace radix_topk_amd_trace
+#define TOPK_TRACE(id)                                                                         \
+  do {                                                                                         \
+    if (threadIdx.x == 0 && blockIdx.x < radix_topk_amd_trace::kMaxWorkgroups) {               \
+      unsigned long long* row_ = radix_topk_amd_trace::g_clock + blockIdx.x * 16;              \
+      unsigned long long* real_ = radix_topk_amd_trace::g_real + blockIdx.x * 16;              \
+      if ((id) == 0)                                                                           \
+        for (int q_ = 1; q_ < 16; ++q_) row_[q_] = real_[q_] = 0;                              \
+      row_[(id)] = __builtin_amdgcn_s_memtime();                                               \
+      real_[(id)] = __builtin_amdgcn_s_memrealtime();                                          \
+    }                                                                                          \
+  } while (0)
+#define TOPK_WTRACE(id)                                                                        \
+  do {                                                                                         \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < radix_topk_amd_trace::kMaxWorkgroups)          \
+      radix_topk_amd_trace::g_wave[(blockIdx.x * 16 + (threadIdx.x >> 6)) * 16 + (id)] =       \
+          __builtin_amdgcn_s_memtime();                                                        \
+  } while (0)
+#define TOPK_TRACE_VALUE(id, value)                                                            \
+  do {                                                                                         \
+    if (threadIdx.x == 0 && blockIdx.x < radix_topk_amd_trace::kMaxWorkgroups)                 \
+      radix_topk_amd_trace::g_clock[blockIdx.x * 16 + (id)] = (value);                         \
+  } while (0)
+#else
 #define TOPK_TRACE(id)
-#endif
-#ifndef TOPK_WTRACE
 #define TOPK_WTRACE(id)
-#endif
-#ifndef TOPK_TRACE_VALUE
 #define TOPK_TRACE_VALUE(id, value)
 #endif
 
@@ -756,6 +792,7 @@ __device__ u32 group_collect(const u64* counts, const u64* lists, u64 tag, int a
     if (lane == 63) scal[0] = static_cast<int>(incl);
   }
   __syncthreads();
+  TOPK_TRACE(3);
   const u32 total = static_cast<u32>(scal[0]);
   if (total > static_cast<u32>(kGroupCap)) return kAbsent;
   // All of a thread's entries are located first and then loaded together, so their latencies
@@ -787,6 +824,7 @@ __device__ u32 group_collect(const u64* counts, const u64* lists, u64 tag, int a
     if (i < total) area[i] = val[r];
   }
   __syncthreads();
+  TOPK_TRACE(7);
   return total;
 }
 
@@ -1662,3 +1700,23 @@ int launch_segmented_topk(const Plan& plan, const TopkParams& params, void* stre
 }
 
 }  // namespace radix_topk_amd
+
+#ifdef TOPK_PHASE_TRACE
+// Profiling build only: copies the phase tables to host buffers (kMaxWorkgroups x 16 words each
+// for the workgroup tables, x 16 x 16 for the wave table), or zeroes them.
+extern "C" int radix_topk_trace_fetch(void* clock, void* real, void* wave) {
+  using namespace radix_topk_amd_trace;
+  hipError_t e = hipMemcpyFromSymbol(clock, HIP_SYMBOL(g_clock), sizeof(g_clock));
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(real, HIP_SYMBOL(g_real), sizeof(g_real));
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(wave, HIP_SYMBOL(g_wave), sizeof(g_wave));
+  return static_cast<int>(e);
+}
+extern "C" int radix_topk_trace_clear() {
+  using namespace radix_topk_amd_trace;
+  static unsigned long long zeros[kMaxWorkgroups * 16 * 16];
+  hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_clock), zeros, sizeof(g_clock));
+  if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(g_real), zeros, sizeof(g_real));
+  if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(g_wave), zeros, sizeof(g_wave));
+  return static_cast<int>(e);
+}
+#endif

@@ -24,6 +24,13 @@
   python -m batch_topk_amd.profiling matrix [--out FILE]
       bench.py over every workload (fp16; bf16 and the sampling consumer on the LLM logits;
       fp32 on every workload; the unsorted and indices-only outputs), as a markdown table.
+
+  python -m batch_topk_amd.profiling phases [--workload W] [--k K] [--b2b N]
+      Step timeline of the top-k kernel on an fp16 workload, from the phase-traced build of
+      the engine (libbatch_topk_amd_trace.so): per-workgroup stamps of the last of N
+      back-to-back calls, on the GPU's constant 100 MHz clock from the first workgroup's
+      start, and per-wave stamps on the shader clock from the wave's workgroup start.  The
+      stamps cost time themselves (the traced build runs about 1 us slower per call).
 """
 
 from __future__ import annotations
@@ -123,6 +130,117 @@ def run_floor(calls: int) -> None:
         print(f"{w} | {block} x {vpt} | {us:.2f} | {nbytes / us / 1e3:.0f} | {nbytes / us / 1e3 / 8000:.3f}")
 
 
+PHASES = ((12, "loads issued"), (1, "thread best"), (2, "first histogram round"),
+          (8, "first meeting / list published"), (9, "cooperative threshold"), (4, "threshold"),
+          (5, "filter"), (6, "refinement done"), (10, "list stored / lists merged"),
+          (3, "cooperative lengths read"), (7, "cooperative lists gathered"), (11, "end"))
+WAVE_PHASES = ((1, "thread best"), (0, "threshold read"), (2, "filter start"), (3, "vectors staged"),
+               (4, "flushed"), (5, "after filter barrier"), (6, "ranking start"), (7, "ranking end"))
+
+
+def run_phases(workload: str, k: int, b2b: int) -> None:
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from batch_topk_amd import build, workloads
+
+    lib = ctypes.CDLL(build.TRACE_LIB_PATH)
+    vp, i32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    lib.radix_topk_trace_fetch.argtypes = [vp, vp, vp]
+    lib.radix_topk_trace_fetch.restype = i32
+    lib.radix_topk_trace_clear.argtypes = []
+    lib.radix_topk_trace_clear.restype = i32
+    out = getattr(workloads, workload)()
+    if isinstance(out, tuple):  # varlen: (bits, offsets)
+        bits, offsets = out
+        seg_num, max_len = offsets.size - 1, int(np.diff(offsets).max())
+    else:
+        bits, offsets = out, None
+        seg_num, max_len = bits.shape
+    dev = "cuda:0"
+    src = torch.from_numpy(np.ascontiguousarray(bits).reshape(-1).view(np.int16)).to(dev)
+    copies = [src] + [src.clone() for _ in range(max(1, -(-512 * 2**20 // (2 * src.numel()))) - 1)]
+    vals = torch.empty((seg_num, k), dtype=torch.int16, device=dev)
+    idx = torch.empty((seg_num, k), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    if offsets is None:
+        lib.radix_topk_batch_topk_half_workspace_size.restype = sz
+        lib.radix_topk_batch_topk_half_workspace_size.argtypes = [i32, i32, i32]
+        lib.radix_topk_batch_topk_half.argtypes = [vp, i32, i32, i32, vp, vp, vp, sz, vp]
+        wsb = lib.radix_topk_batch_topk_half_workspace_size(seg_num, max_len, k)
+    else:
+        lib.radix_topk_batch_topk_half_segmented_workspace_size.restype = sz
+        lib.radix_topk_batch_topk_half_segmented_workspace_size.argtypes = [i32, i32, i32]
+        lib.radix_topk_batch_topk_half_segmented.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, sz, vp]
+        wsb = lib.radix_topk_batch_topk_half_segmented_workspace_size(seg_num, max_len, k)
+        d_off = torch.from_numpy(offsets.astype(np.int32)).to(dev)
+    ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=dev)
+
+    def call(i):
+        x = copies[i % len(copies)].data_ptr()
+        if offsets is None:
+            rc = lib.radix_topk_batch_topk_half(x, seg_num, max_len, k, vals.data_ptr(), idx.data_ptr(),
+                                                ws.data_ptr(), wsb, stream)
+        else:
+            rc = lib.radix_topk_batch_topk_half_segmented(x, d_off.data_ptr(), seg_num, max_len, k,
+                                                          vals.data_ptr(), idx.data_ptr(), ws.data_ptr(), wsb, stream)
+        if rc != 0:
+            raise RuntimeError(f"top-k call returned {rc}")
+
+    for i in range(30):
+        call(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(200):
+        call(i)
+    b.record()
+    torch.cuda.synchronize()
+    print(f"{workload} k={k}, phase-traced build: {a.elapsed_time(b) * 1e3 / 200:.2f} us per call back-to-back")
+    nwg, nslot = 2048, 16
+    clock = np.zeros(nwg * nslot, np.uint64)
+    real = np.zeros(nwg * nslot, np.uint64)
+    wave = np.zeros(nwg * nslot * 16, np.uint64)
+    if lib.radix_topk_trace_clear() != 0:
+        raise RuntimeError("trace clear failed")
+    for i in range(b2b):
+        call(i)
+    torch.cuda.synchronize()
+    if lib.radix_topk_trace_fetch(clock.ctypes.data, real.ctypes.data, wave.ctypes.data) != 0:
+        raise RuntimeError("trace fetch failed")
+    C = clock.reshape(nwg, nslot).astype(np.int64)
+    R = real.reshape(nwg, nslot).astype(np.int64)
+    W = wave.reshape(nwg, nslot, 16).astype(np.int64)
+    g = np.nonzero(R[:, 0])[0]
+    C, R, W = C[g], R[g], W[g]
+    r0 = R[:, 0].min()
+    print(f"last of {b2b} back-to-back calls: {len(g)} workgroups stamped")
+    print("workgroup step (ns from the first workgroup's start) | stamped | min | median | p90 | max")
+
+    def row(name, d):
+        print(f"{name} | {d.size} | {d.min():.0f} | {np.median(d):.0f} | {np.percentile(d, 90):.0f} | {d.max():.0f}")
+
+    row("start", (R[:, 0] - r0) * 10.0)
+    stamped = [(np.median(R[R[:, j] > 0, j]), j, name) for j, name in PHASES if np.any(R[:, j] > 0)]
+    for _, j, name in sorted(stamped):  # in the order the steps ran
+        m = R[:, j] > 0
+        row(name, (R[m, j] - r0) * 10.0)
+    end = np.where(R[:, 11] > 0, R[:, 11], R.max(axis=1))
+    ok = (C[:, 11] > C[:, 0]) & (end > R[:, 0])
+    if ok.any():
+        ticks_per_ns = np.median((C[ok, 11] - C[ok, 0]) / ((R[ok, 11] - R[ok, 0]) * 10.0))
+        print(f"wave step (ns from its workgroup's start; shader clock {ticks_per_ns * 1e3:.0f} MHz) | stamped | min | median | p90 | max")
+        for j, name in WAVE_PHASES:
+            m = W[:, :, j] > 0
+            if m.any():
+                row(name, ((W[:, :, j] - C[:, 0:1]) / ticks_per_ns)[m])
+    cand = C[:, 14][C[:, 14] > 0]
+    if cand.size:
+        print(f"candidates per workgroup: min {cand.min()} median {np.median(cand):.0f} max {cand.max()}")
+
+
 MATRIX = (
     ("llm_logits", ["--k", "50"]),
     ("uniform_small", ["--k", "50"]),
@@ -199,7 +317,15 @@ def main(argv=None) -> int:
     fl.add_argument("--calls", type=int, default=2000)
     mx = sub.add_parser("matrix")
     mx.add_argument("--out", default=None)
+    ph = sub.add_parser("phases")
+    ph.add_argument("--workload", default="llm_logits")
+    ph.add_argument("--k", type=int, default=50)
+    ph.add_argument("--b2b", type=int, default=20)
     a = ap.parse_args(argv)
+
+    if a.cmd == "phases":
+        run_phases(a.workload, a.k, a.b2b)
+        return 0
 
     if a.cmd == "floor":
         run_floor(a.calls)

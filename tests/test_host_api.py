@@ -35,6 +35,24 @@ def test_library_exports_every_declared_symbol():
     assert set(decl) <= exported
 
 
+def test_phase_trace_hooks_only_in_the_measurement_build():
+    # The per-phase clock stamps are compiled into libbatch_topk_amd_trace.so (loaded by
+    # batch_topk_amd.profiling only); the engine library has no trace entry point.
+    from batch_topk_amd import build
+
+    def defined(path):
+        out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                             check=True).stdout
+        return set(line.split()[-1] for line in out.splitlines() if " T " in line)
+
+    if not os.path.exists(build.TRACE_LIB_PATH):
+        pytest.skip("measurement libraries not built")
+    trace = defined(build.TRACE_LIB_PATH)
+    assert {"radix_topk_trace_fetch", "radix_topk_trace_clear"} <= trace
+    assert set(declared_symbols()) <= trace
+    assert not any("trace" in name for name in defined(bt.LIB_PATH))
+
+
 def test_cpp_dropin_header_forwards_to_c_abi(tmp_path):
     # The C++ drop-in (include/batch_topk.hpp) compiles against HIP headers and adds no symbols.
     src = tmp_path / "use.cpp"
