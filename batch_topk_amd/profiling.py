@@ -25,7 +25,7 @@
       bench.py over every workload (fp16; bf16 and the sampling consumer on the LLM logits;
       fp32 on every workload; the unsorted and indices-only outputs), as a markdown table.
 
-  python -m batch_topk_amd.profiling phases [--workload W] [--k K] [--b2b N]
+  python -m batch_topk_amd.profiling phases [--workload W | --shape SEGxLEN] [--k K] [--b2b N]
       Step timeline of the top-k kernel on an fp16 workload, from the phase-traced build of
       the engine (libbatch_topk_amd_trace.so): per-workgroup stamps of the last of N
       back-to-back calls, on the GPU's constant 100 MHz clock from the first workgroup's
@@ -138,7 +138,7 @@ WAVE_PHASES = ((1, "thread best"), (0, "threshold read"), (2, "filter start"), (
                (4, "flushed"), (5, "after filter barrier"), (6, "ranking start"), (7, "ranking end"))
 
 
-def run_phases(workload: str, k: int, b2b: int) -> None:
+def run_phases(workload: str, k: int, b2b: int, shape: str | None = None) -> None:
     import ctypes
 
     import numpy as np
@@ -152,7 +152,13 @@ def run_phases(workload: str, k: int, b2b: int) -> None:
     lib.radix_topk_trace_fetch.restype = i32
     lib.radix_topk_trace_clear.argtypes = []
     lib.radix_topk_trace_clear.restype = i32
-    out = getattr(workloads, workload)()
+    if shape:  # SEGxLEN of N(0, 1) fp16, seed 0
+        seg_num_s, seg_len_s = (int(v) for v in shape.lower().split("x"))
+        rng = np.random.default_rng(0)
+        out = rng.standard_normal((seg_num_s, seg_len_s), dtype=np.float32).astype(np.float16).view(np.uint16)
+        workload = f"N(0,1) {seg_num_s}x{seg_len_s}"
+    else:
+        out = getattr(workloads, workload)()
     if isinstance(out, tuple):  # varlen: (bits, offsets)
         bits, offsets = out
         seg_num, max_len = offsets.size - 1, int(np.diff(offsets).max())
@@ -321,10 +327,11 @@ def main(argv=None) -> int:
     ph.add_argument("--workload", default="llm_logits")
     ph.add_argument("--k", type=int, default=50)
     ph.add_argument("--b2b", type=int, default=20)
+    ph.add_argument("--shape", default=None, help="SEGxLEN of N(0,1) fp16 instead of a workload")
     a = ap.parse_args(argv)
 
     if a.cmd == "phases":
-        run_phases(a.workload, a.k, a.b2b)
+        run_phases(a.workload, a.k, a.b2b, a.shape)
         return 0
 
     if a.cmd == "floor":
