@@ -462,30 +462,32 @@ __device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u
   }
 }
 
-// Ranks the M (<= 128) unique candidates of `list` and writes those of rank < kk (also to
-// sorted[rank] when sorted is not null).  One DPP
-// row (16 lanes) per candidate: lane q of the row compares it with entries q, q + 16, ... (held
-// in registers, loaded once), and a row prefix sum leaves its rank in the row's last lane,
-// which writes the output entry.  The rows take the candidates in turn.
-template <int BLOCK, class E>
+// Ranks the M (<= 16 * S) unique candidates of `list` and writes those of rank < kk (also to
+// sorted[rank] when sorted is not null).  One DPP row (16 lanes) per candidate: lane q of the
+// row compares it with entries q, q + 16, ... (S of them, held in registers, loaded once), and
+// a row prefix sum leaves its rank in the row's last lane, which writes the output entry.  The
+// rows take the candidates in turn.  The S loads are unconditional (all inside the candidate
+// area) and masked past M, so the slot count, not branches, bounds the work.
+template <int BLOCK, int S, class E>
 __device__ void row_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M, int kk,
                                u64* sorted) {
+  static_assert(16 * S <= kArea, "the unconditional loads stay inside the candidate area");
   constexpr int ROWS = BLOCK / 16;
   const int row = threadIdx.x >> 4;
   const int q = threadIdx.x & 15;
-  u64 ent[8];
+  u64 ent[S];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
+  for (int t = 0; t < S; ++t) {
     const int i = q + 16 * t;
-    ent[t] = ~0ull;
-    if (16 * t < M) ent[t] = i < M ? list[i] : ~0ull;  // uniform: no LDS read past the list
+    const u64 e = list[i];
+    ent[t] = i < M ? e : ~0ull;
   }
   TOPK_WTRACE(6);
   for (int c = row; c < M; c += ROWS) {  // uniform within each row
     const u64 x = list[c];
     u32 cnt = 0;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) cnt += ent[t] < x ? 1u : 0u;
+    for (int t = 0; t < S; ++t) cnt += ent[t] < x ? 1u : 0u;
     cnt += dpp<0x111, 0xf>(cnt);
     cnt += dpp<0x112, 0xf>(cnt);
     cnt += dpp<0x114, 0xf>(cnt);
@@ -531,7 +533,11 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
   u64* sorted = sm.sel;
   // Small sets: one DPP row per candidate counts the smaller entries (row_rank_write).
   if (M <= 128) {
-    row_rank_write<BLOCK, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+    if (M <= 64) {
+      row_rank_write<BLOCK, 4, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+    } else {
+      row_rank_write<BLOCK, 8, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+    }
   } else if (p.unsorted && !sampling) {
     // Unsorted output: the kk best, found by radix select, in the order they are found.
     if (M > kk) {
