@@ -24,9 +24,10 @@
 //                      (key, index), and the raw bits ride along to the output.
 //                      If the list overflows (ties, all-equal rows), an exact radix refinement
 //                      over (key16, position17), re-reading the chunk, rebuilds it.
-//   4. selection       small sets: every wave holds the whole list in registers, ranks its
-//                      share by ballot counts and writes it; larger sets: LDS radix select over
-//                      the packed values down to exactly k, then rank counting.
+//   4. selection       small sets: every candidate counts the entries below it (one DPP row
+//                      per candidate up to 128; up to 32 entries per wave, one lane per
+//                      candidate over 16-byte LDS broadcasts); larger sets: LDS radix select
+//                      over the packed values down to exactly k, then rank counting.
 //   5. output          index and raw value bits of each selected candidate.
 //
 // Segments longer than one chunk are split over W workgroups.  While the W lists fit one LDS
@@ -418,47 +419,78 @@ __device__ void block_rank(const u64* v, int M, int* rank) {
   __syncthreads();
 }
 
-// Ranks the M (<= 64 * S) unique candidates of `list` and stores those of rank < kk at
-// sel[rank].  Every wave holds the whole list in registers (S u64 per lane) and ranks its
-// share of the candidates with ballots: rank(x) = sum over slots of popcount(ballot(c < x)).
-template <int BLOCK, int S, class E>
-__device__ void wave_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
-                                int kk, u64* sorted) {
+// Ranks the M unique entries of `list` (LDS, 16-byte aligned, M <= rank capacity) and writes
+// those of rank < kk to the segment's output row (also to sorted[rank] when sorted is not
+// null); rank(x) = #{j : list[j] < x}.  A wave takes 64 candidates, one per lane, and a share
+// of the entries, which it reads as wave-uniform 16-byte LDS broadcasts (two entries each);
+// every lane counts the entries below its candidate with one 64-bit compare and one add per
+// entry.  That spreads the M * M comparisons over the VALUs of all four SIMDs instead of
+// issuing a ballot popcount per (candidate, 64 entries) on the CU's single scalar unit.  With
+// fewer candidate groups than waves, the entry range is split between waves and the partial
+// counts are summed in rank[] (LDS, M ints) before the writes.
+template <int BLOCK, class E>
+__device__ void lds_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
+                               int kk, int* rank, u64* sorted) {
+  typedef u64 u64x2_t __attribute__((ext_vector_type(2)));
   constexpr int NW = BLOCK / 64;
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
-  u64 c[S];
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    const int i = s * 64 + lane;
-    c[s] = i < M ? list[i] : ~0ull;
+  const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int G = (M + 63) >> 6;                  // candidate groups of 64
+  const int Q = G >= NW ? 1 : NW / G;           // waves sharing one group's entry range
+  const int span = ((M + Q - 1) / Q + 7) & ~7;  // entries per share, a multiple of 8
+  if (Q > 1) {
+    for (int i = threadIdx.x; i < M; i += BLOCK) rank[i] = 0;
+    __syncthreads();
   }
-  const int slots = (M + 63) >> 6;
-  // This wave's candidates are i = wid + NW * t; lane t fetches the t-th one, so all of them
-  // come from LDS in one round, and each is then broadcast with a lane read.  Its rank (the
-  // number of smaller entries) lands back in lane t, which writes the output row directly.
-  constexpr int PER = 64 * S / NW;  // upper bound of candidates per wave (M <= 64 * S)
-  static_assert(PER <= 64, "one candidate per lane");
-  const int mine_i = wid + NW * lane;
-  const u64 mine = (lane < PER && mine_i < M) ? list[mine_i] : ~0ull;
-  const int count = M > wid ? (M - wid + NW - 1) / NW : 0;
   TOPK_WTRACE(6);
-  int my_rank = kk;
-  for (int t = 0; t < count; ++t) {
-    const u32 xl = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(mine)), t));
-    const u32 xh = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(mine >> 32)), t));
-    const u64 x = (static_cast<u64>(xh) << 32) | xl;
-    int r = 0;
+  const u64x2_t* pairs = reinterpret_cast<const u64x2_t*>(list);
+  for (int u = wid; u < G * Q; u += NW) {
+    const int g = u % G;
+    const int q = u / G;
+    const int i = g * 64 + lane;
+    const u64 x = i < M ? list[i] : 0ull;
+    const int j0 = q * span;
+    const int j1 = j0 + span < M ? j0 + span : M;
+    u32 c = 0;
+    int j = j0;
+    // 16 entries (eight reads in flight) per step, then one step of 8: the loop is bound by
+    // LDS latency, not by the compares, when a SIMD holds only two waves.
+    for (; j + 16 <= j1; j += 16) {
+      u64x2_t a[8];
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-      if (s < slots) r += __popcll(ballot(c[s] < x));
+      for (int e = 0; e < 8; ++e) a[e] = pairs[(j >> 1) + e];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c += (a[e].x < x ? 1u : 0u) + (a[e].y < x ? 1u : 0u);
     }
-    my_rank = lane == t ? r : my_rank;
+    if (j + 8 <= j1) {
+      u64x2_t a[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = pairs[(j >> 1) + e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c += (a[e].x < x ? 1u : 0u) + (a[e].y < x ? 1u : 0u);
+      j += 8;
+    }
+    for (; j < j1; ++j) c += list[j] < x ? 1u : 0u;
+    if (Q == 1) {
+      if (i < M && c < static_cast<u32>(kk)) {
+        write_rank<E>(p, n, seg, static_cast<int>(c), x);
+        if (sorted) sorted[c] = x;
+      }
+    } else if (i < M && c) {
+      atomicAdd(&rank[i], static_cast<int>(c));
+    }
   }
   TOPK_WTRACE(7);
-  if (lane < count && my_rank < kk) {
-    write_rank<E>(p, n, seg, my_rank, mine);
-    if (sorted) sorted[my_rank] = mine;
+  if (Q > 1) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < M; i += BLOCK) {
+      const int r = rank[i];
+      if (r < kk) {
+        const u64 x = list[i];
+        write_rank<E>(p, n, seg, r, x);
+        if (sorted) sorted[r] = x;
+      }
+    }
   }
 }
 
@@ -551,11 +583,12 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
     } else {
       for (int i = tid; i < M; i += BLOCK) write_rank<E>(p, n, seg, i, sm.area[i]);
     }
-  } else if (NW >= 8 && M <= 8 * NW * 4 && M <= 512) {
-    // Up to 512: every wave ranks its share against the whole list held in registers (a radix
-    // select first, then ranking only kk, was measured no faster: tied keys take the select
-    // through the index digits, and the extra ranking code slows the other paths).
-    if constexpr (NW >= 8) wave_rank_write<BLOCK, 8, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+  } else if (NW >= 8 && M <= 32 * NW && M <= kRankCap) {
+    // Up to 32 entries per wave: rank the whole list (a radix select first, then ranking only
+    // kk, was measured no faster: tied keys take the select through the index digits).  Longer
+    // lists take the select: with 8 waves, ranking 512 entries in full (8 latency-bound LDS
+    // passes per wave, two waves per SIMD) ran 66.7 -> 112.3 us on 6000 x 10000, k = 50.
+    lds_rank_write<BLOCK, E>(p, n, seg, sm.area, M, kk, sm.rank, sampling ? sorted : nullptr);
   } else {
     const u64* sel = sm.area;
     if (M > kk) {
@@ -573,6 +606,9 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
       sel = sm.sel;
       sorted = sm.area;  // the candidates are no longer needed
     }
+    // The kk selected entries: one thread per (entry, slice of the selection); ranking
+    // them with lds_rank_write instead was measured slower on many short segments
+    // (6000 x 10000, k = 50: 66.4 -> 68.0 us).
     block_rank<BLOCK>(sel, kk, sm.rank);
     for (int i = tid; i < kk; i += BLOCK) {
       write_rank<E>(p, n, seg, sm.rank[i], sel[i]);
