@@ -421,10 +421,10 @@ __device__ void block_rank(const u64* v, int M, int* rank) {
 
 // Ranks the M unique entries of `list` (LDS, 16-byte aligned, M <= rank capacity) and writes
 // those of rank < kk to the segment's output row (also to sorted[rank] when sorted is not
-// null); rank(x) = #{j : list[j] < x}.  A wave takes 64 candidates, one per lane, and a share
+// null); rank(x) = #{j : list[j] < x}.  A wave takes 128 candidates, two per lane, and a share
 // of the entries, which it reads as wave-uniform 16-byte LDS broadcasts (two entries each);
-// every lane counts the entries below its candidate with one 64-bit compare and one add per
-// entry.  That spreads the M * M comparisons over the VALUs of all four SIMDs instead of
+// every lane counts the entries below each of its candidates with one 64-bit compare and one
+// add per entry.  That spreads the M * M comparisons over the VALUs of all four SIMDs instead of
 // issuing a ballot popcount per (candidate, 64 entries) on the CU's single scalar unit.  With
 // fewer candidate groups than waves, the entry range is split between waves and the partial
 // counts are summed in rank[] (LDS, M ints) before the writes.
@@ -435,7 +435,7 @@ __device__ void lds_rank_write(const TopkParams& p, int64_t n, int seg, const u6
   constexpr int NW = BLOCK / 64;
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int G = (M + 63) >> 6;                  // candidate groups of 64
+  const int G = (M + 127) >> 7;                 // candidate groups of 128 (two per lane)
   const int Q = G >= NW ? 1 : NW / G;           // waves sharing one group's entry range
   const int span = ((M + Q - 1) / Q + 7) & ~7;  // entries per share, a multiple of 8
   if (Q > 1) {
@@ -447,11 +447,13 @@ __device__ void lds_rank_write(const TopkParams& p, int64_t n, int seg, const u6
   for (int u = wid; u < G * Q; u += NW) {
     const int g = u % G;
     const int q = u / G;
-    const int i = g * 64 + lane;
-    const u64 x = i < M ? list[i] : 0ull;
+    const int i0 = g * 128 + lane;
+    const int i1 = i0 + 64;
+    const u64 x0 = i0 < M ? list[i0] : 0ull;
+    const u64 x1 = i1 < M ? list[i1] : 0ull;
     const int j0 = q * span;
     const int j1 = j0 + span < M ? j0 + span : M;
-    u32 c = 0;
+    u32 c0 = 0, c1 = 0;
     int j = j0;
     // 16 entries (eight reads in flight) per step, then one step of 8: the loop is bound by
     // LDS latency, not by the compares, when a SIMD holds only two waves.
@@ -460,24 +462,39 @@ __device__ void lds_rank_write(const TopkParams& p, int64_t n, int seg, const u6
 #pragma unroll
       for (int e = 0; e < 8; ++e) a[e] = pairs[(j >> 1) + e];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) c += (a[e].x < x ? 1u : 0u) + (a[e].y < x ? 1u : 0u);
+      for (int e = 0; e < 8; ++e) {
+        c0 += (a[e].x < x0 ? 1u : 0u) + (a[e].y < x0 ? 1u : 0u);
+        c1 += (a[e].x < x1 ? 1u : 0u) + (a[e].y < x1 ? 1u : 0u);
+      }
     }
     if (j + 8 <= j1) {
       u64x2_t a[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) a[e] = pairs[(j >> 1) + e];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) c += (a[e].x < x ? 1u : 0u) + (a[e].y < x ? 1u : 0u);
+      for (int e = 0; e < 4; ++e) {
+        c0 += (a[e].x < x0 ? 1u : 0u) + (a[e].y < x0 ? 1u : 0u);
+        c1 += (a[e].x < x1 ? 1u : 0u) + (a[e].y < x1 ? 1u : 0u);
+      }
       j += 8;
     }
-    for (; j < j1; ++j) c += list[j] < x ? 1u : 0u;
+    for (; j < j1; ++j) {
+      const u64 v = list[j];
+      c0 += v < x0 ? 1u : 0u;
+      c1 += v < x1 ? 1u : 0u;
+    }
     if (Q == 1) {
-      if (i < M && c < static_cast<u32>(kk)) {
-        write_rank<E>(p, n, seg, static_cast<int>(c), x);
-        if (sorted) sorted[c] = x;
+      if (i0 < M && c0 < static_cast<u32>(kk)) {
+        write_rank<E>(p, n, seg, static_cast<int>(c0), x0);
+        if (sorted) sorted[c0] = x0;
       }
-    } else if (i < M && c) {
-      atomicAdd(&rank[i], static_cast<int>(c));
+      if (i1 < M && c1 < static_cast<u32>(kk)) {
+        write_rank<E>(p, n, seg, static_cast<int>(c1), x1);
+        if (sorted) sorted[c1] = x1;
+      }
+    } else {
+      if (i0 < M && c0) atomicAdd(&rank[i0], static_cast<int>(c0));
+      if (i1 < M && c1) atomicAdd(&rank[i1], static_cast<int>(c1));
     }
   }
   TOPK_WTRACE(7);
