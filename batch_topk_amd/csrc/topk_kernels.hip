@@ -425,9 +425,9 @@ __device__ void block_rank(const u64* v, int M, int* rank) {
 // of the entries, which it reads as wave-uniform 16-byte LDS broadcasts (two entries each);
 // every lane counts the entries below each of its candidates with one 64-bit compare and one
 // add per entry.  That spreads the M * M comparisons over the VALUs of all four SIMDs instead of
-// issuing a ballot popcount per (candidate, 64 entries) on the CU's single scalar unit.  With
-// fewer candidate groups than waves, the entry range is split between waves and the partial
-// counts are summed in rank[] (LDS, M ints) before the writes.
+// issuing a ballot popcount per (candidate, 64 entries) on the CU's single scalar unit.  The
+// entry range is split between the waves that share a candidate group, and the partial counts
+// are summed in rank[] (LDS, M ints) before the writes.
 template <int BLOCK, class E>
 __device__ void lds_rank_write(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
                                int kk, int* rank, u64* sorted) {
@@ -438,10 +438,8 @@ __device__ void lds_rank_write(const TopkParams& p, int64_t n, int seg, const u6
   const int G = (M + 127) >> 7;                 // candidate groups of 128 (two per lane)
   const int Q = G >= NW ? 1 : NW / G;           // waves sharing one group's entry range
   const int span = ((M + Q - 1) / Q + 7) & ~7;  // entries per share, a multiple of 8
-  if (Q > 1) {
-    for (int i = threadIdx.x; i < M; i += BLOCK) rank[i] = 0;
-    __syncthreads();
-  }
+  for (int i = threadIdx.x; i < M; i += BLOCK) rank[i] = 0;
+  __syncthreads();
   TOPK_WTRACE(6);
   const u64x2_t* pairs = reinterpret_cast<const u64x2_t*>(list);
   for (int u = wid; u < G * Q; u += NW) {
@@ -483,30 +481,17 @@ __device__ void lds_rank_write(const TopkParams& p, int64_t n, int seg, const u6
       c0 += v < x0 ? 1u : 0u;
       c1 += v < x1 ? 1u : 0u;
     }
-    if (Q == 1) {
-      if (i0 < M && c0 < static_cast<u32>(kk)) {
-        write_rank<E>(p, n, seg, static_cast<int>(c0), x0);
-        if (sorted) sorted[c0] = x0;
-      }
-      if (i1 < M && c1 < static_cast<u32>(kk)) {
-        write_rank<E>(p, n, seg, static_cast<int>(c1), x1);
-        if (sorted) sorted[c1] = x1;
-      }
-    } else {
-      if (i0 < M && c0) atomicAdd(&rank[i0], static_cast<int>(c0));
-      if (i1 < M && c1) atomicAdd(&rank[i1], static_cast<int>(c1));
-    }
+    if (i0 < M && c0) atomicAdd(&rank[i0], static_cast<int>(c0));
+    if (i1 < M && c1) atomicAdd(&rank[i1], static_cast<int>(c1));
   }
   TOPK_WTRACE(7);
-  if (Q > 1) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < M; i += BLOCK) {
-      const int r = rank[i];
-      if (r < kk) {
-        const u64 x = list[i];
-        write_rank<E>(p, n, seg, r, x);
-        if (sorted) sorted[r] = x;
-      }
+  __syncthreads();
+  for (int i = threadIdx.x; i < M; i += BLOCK) {
+    const int r = rank[i];
+    if (r < kk) {
+      const u64 x = list[i];
+      write_rank<E>(p, n, seg, r, x);
+      if (sorted) sorted[r] = x;
     }
   }
 }
