@@ -46,7 +46,13 @@ EXPORTED_SYMBOLS = (
     "radix_topk_batch_topk_f32_workspace_size",
     "radix_topk_batch_topk_f32_segmented",
     "radix_topk_batch_topk_f32_segmented_workspace_size",
+    "radix_topk_workspace_status",
+    "radix_topk_debug_wait_hook",
 )
+
+# radix_topk_workspace_status codes (include/batch_topk.h)
+STATUS_OK = 0
+STATUS_WAIT_TIMEOUT = 1
 
 # radix_topk_batch_topk_ex element formats and output flags (include/batch_topk.h)
 FORMAT_F16 = 0
@@ -111,6 +117,10 @@ def load_library():
         L.radix_topk_batch_topk_ex.argtypes = [vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, sz, vp]
         L.radix_topk_batch_topk_ex_workspace_size.restype = sz
         L.radix_topk_batch_topk_ex_workspace_size.argtypes = [i32, i32, i32, i32, i32]
+        L.radix_topk_workspace_status.restype = i32
+        L.radix_topk_workspace_status.argtypes = [vp, sz, i32, vp, vp]
+        L.radix_topk_debug_wait_hook.restype = None
+        L.radix_topk_debug_wait_hook.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
         _lib = L
     return _lib
 
@@ -239,6 +249,22 @@ def batch_topk_ex_workspace_size(fmt: int, segmented: bool, seg_num: int, seg_le
                                                                       seg_num, seg_len, k))
 
 
+def workspace_status(d_workspace: int, workspace_bytes: int, seg_num: int, stream: int = 0):
+    """radix_topk_workspace_status: per-segment status words of the last call made with the
+    workspace (STATUS_OK or STATUS_WAIT_TIMEOUT), as a list; synchronises ``stream``."""
+    buf = (ctypes.c_uint32 * max(1, seg_num))()
+    rc = int(load_library().radix_topk_workspace_status(d_workspace, workspace_bytes, seg_num, buf, stream))
+    if rc != HIP_SUCCESS:
+        raise TopkError(rc, "radix_topk_workspace_status")
+    return [int(v) for v in buf[:seg_num]]
+
+
+def debug_wait_hook(spin_limit: int, force_mask: int = 0) -> None:
+    """radix_topk_debug_wait_hook (test hook): bound every cross-workgroup wait at spin_limit
+    polls and force the waits named by force_mask to time out; (0, 0) restores ordinary calls."""
+    load_library().radix_topk_debug_wait_hook(spin_limit, force_mask)
+
+
 # ------------------------------------------------------------------ torch conveniences
 
 def _entry_points(dtype):
@@ -255,6 +281,18 @@ def _entry_points(dtype):
         return (batch_topk_f32, batch_topk_f32_workspace_size, batch_topk_f32_segmented,
                 batch_topk_f32_segmented_workspace_size)
     raise ValueError(f"unsupported dtype {dtype}: float16, bfloat16 or float32")
+
+
+def _on_stream(stream):
+    """Makes ``stream`` current while a call allocates its outputs and temporary workspace, so
+    that torch's caching allocator ties them to the stream the kernel runs on (a temporary freed
+    on return is then reused only by work ordered after the kernel)."""
+    import contextlib
+
+    import torch
+
+    return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+
 
 def _stream_handle(stream) -> int:
     import torch
@@ -301,7 +339,14 @@ def topk(x, k: int, workspace=None, stream=None, sorted: bool = True, values: bo
     Returns (values [seg_num, k] of x's dtype, indices int32 [seg_num, k]).  ``workspace``
     may be a uint8 CUDA tensor of at least the workspace size of the shape.  ``sorted=False``
     returns each row's top-k in unspecified order; ``values=False`` returns (None, indices).
+    ``stream`` (a torch.cuda.Stream, default the current one) runs the kernel; the outputs are
+    allocated on it.
     """
+    with _on_stream(stream):
+        return _topk(x, k, workspace, stream, sorted, values)
+
+
+def _topk(x, k, workspace, stream, sorted, values):
     import torch
 
     if x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
@@ -330,8 +375,14 @@ def segmented_topk(x, offsets, k: int, max_seg_len: int, workspace=None, stream=
     CUDA tensor.
 
     ``offsets`` is an int32 CUDA tensor of seg_num + 1 entries.  Ranks beyond a segment's
-    length hold index -1 and value bits 0xFFFF.  ``sorted`` and ``values`` as for topk.
+    length hold index -1 and value bits 0xFFFF.  ``sorted``, ``values`` and ``stream`` as for
+    topk.
     """
+    with _on_stream(stream):
+        return _segmented_topk(x, offsets, k, max_seg_len, workspace, stream, sorted, values)
+
+
+def _segmented_topk(x, offsets, k, max_seg_len, workspace, stream, sorted, values):
     import torch
 
     if not x.is_cuda or not x.is_contiguous():
@@ -364,8 +415,13 @@ def sample(logits, k: int, temperature: float, uniforms, with_probs: bool = Fals
     ``temperature`` with ``uniforms`` (float32 CUDA tensor [seg_num], values in [0, 1)).
 
     Returns (samples int32 [seg_num], top-k values, top-k indices, probs float32
-    [seg_num, k] or None).
+    [seg_num, k] or None).  ``stream`` as for topk.
     """
+    with _on_stream(stream):
+        return _sample(logits, k, temperature, uniforms, with_probs, workspace, stream)
+
+
+def _sample(logits, k, temperature, uniforms, with_probs, workspace, stream):
     import torch
 
     if logits.dim() != 2 or not logits.is_cuda or not logits.is_contiguous():

@@ -115,6 +115,7 @@ Plan make_plan(int seg_num, int64_t max_len, int k, int ev = 8, bool shared_alig
   plan.cooperative = cooperative;
   size_t ws = kAlign;                                        // alignment slack of the carve
   ws += align_up(static_cast<size_t>(seg_num) * 8, kAlign);  // arrival tickets
+  ws += align_up(static_cast<size_t>(seg_num) * 4, kAlign);  // per-segment status words
   if (cooperative) {
     ws += static_cast<size_t>(seg_num) * group_layout(static_cast<int>(W)).bytes;  // group blocks
   } else if (W > 1) {
@@ -143,6 +144,10 @@ uint64_t next_epoch() {
     return e;
   }
 }
+
+// Test hook of the bounded cross-workgroup waits: spin limit << 32 | kForce* bits, or 0 for
+// ordinary calls (radix_topk_debug_wait_hook).
+std::atomic<uint64_t> g_wait_hook{0};
 
 // Top-k sampling request riding on a top-k call (sample_topk).
 struct SampleSpec {
@@ -194,6 +199,8 @@ int run(const Plan& plan, uint32_t inf_bits, const void* d_input, const int32_t*
   size_t off = 0;
   p.tickets = reinterpret_cast<unsigned long long*>(ws + off);
   off += align_up(static_cast<size_t>(seg_num) * 8, kAlign);
+  p.status = reinterpret_cast<uint32_t*>(ws + off);
+  off += align_up(static_cast<size_t>(seg_num) * 4, kAlign);
   p.cooperative = plan.cooperative ? 1 : 0;
   if (plan.cooperative) {
     p.groups = reinterpret_cast<unsigned char*>(ws + off);
@@ -204,6 +211,9 @@ int run(const Plan& plan, uint32_t inf_bits, const void* d_input, const int32_t*
   }
   p.epoch = next_epoch();
   p.inf_bits = inf_bits;
+  const uint64_t hook = g_wait_hook.load(std::memory_order_relaxed);
+  p.spin_limit = hook ? static_cast<uint32_t>(hook >> 32) : kDefaultSpinLimit;
+  p.force_timeout = static_cast<uint32_t>(hook);
   // Sampling is fused into the kernel's last step, except on a cooperative plan (the ranking
   // is spread over the segment's workgroups): there a one-wave-per-row kernel follows.
   if (sample && !plan.cooperative) {
@@ -319,6 +329,22 @@ int sample_topk(bool bf16, const uint16_t* d_logits, int seg_num, int seg_len, i
   const SampleSpec spec{d_uniforms, d_samples, d_probs, inv_t};
   return run(plan, bf16 ? kInfBitsBF16 : kInfBitsF16, d_logits, nullptr, seg_num, seg_len, seg_len, k,
              d_topk_values, d_topk_indices, d_workspace, workspace_bytes, stream, &spec);
+}
+
+// Copies the per-segment status words of the last call made with the workspace (see
+// radix_topk_workspace_status in batch_topk.h).
+int workspace_status(const void* d_workspace, size_t workspace_bytes, int seg_num, uint32_t* h_status,
+                     void* stream) {
+  if (!d_workspace || !h_status || seg_num <= 0) return kInvalid;
+  const uintptr_t ws = align_up(reinterpret_cast<uintptr_t>(d_workspace), kAlign);
+  const size_t off = align_up(static_cast<size_t>(seg_num) * 8, kAlign);
+  const size_t need = (ws - reinterpret_cast<uintptr_t>(d_workspace)) + off + static_cast<size_t>(seg_num) * 4;
+  if (workspace_bytes < need) return kInvalid;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipMemcpyAsync(h_status, reinterpret_cast<const void*>(ws + off),
+                                static_cast<size_t>(seg_num) * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return static_cast<int>(e);
 }
 
 }  // namespace
@@ -441,6 +467,16 @@ int radix_topk_sample_bf16(const uint16_t* d_logits, int seg_num, int seg_len, i
   return radix_topk_amd::sample_topk(true, d_logits, seg_num, seg_len, k, temperature, d_uniforms,
                                      d_topk_values, d_topk_indices, d_probs, d_samples, d_workspace,
                                      workspace_bytes, stream);
+}
+
+int radix_topk_workspace_status(const void* d_workspace, size_t workspace_bytes, int seg_num,
+                                uint32_t* h_status, void* stream) {
+  return radix_topk_amd::workspace_status(d_workspace, workspace_bytes, seg_num, h_status, stream);
+}
+
+void radix_topk_debug_wait_hook(uint32_t spin_limit, uint32_t force_mask) {
+  radix_topk_amd::g_wait_hook.store(
+      spin_limit == 0 ? 0 : ((static_cast<uint64_t>(spin_limit) << 32) | force_mask), std::memory_order_relaxed);
 }
 
 }  // extern "C"

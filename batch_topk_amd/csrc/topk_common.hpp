@@ -19,10 +19,15 @@ constexpr int kMaxChunk = 1024 * 16 * 8;
 
 // Cooperative (whole-segment threshold) path: per-segment workspace block of a segment split
 // over W workgroups.  Nothing in it needs clearing before a call except the histograms, which
-// workgroup 0 clears at the start of the call:
-//   flag    u64                       epoch-tagged "histograms cleared" word
+// workgroup 0 clears at the start of the call.  Every word one workgroup writes for another
+// carries a per-call token derived from the host's call epoch and the block's generation
+// word, which the call advances, so a replayed call (same epoch) never takes a word left by an
+// earlier replay for its own:
+//   flag    u64                       "histograms cleared" word (tag44 << 20 | 1), and at
+//                                     byte 8 the generation word (read by every workgroup at
+//                                     its start, advanced once all have read it)
 //   arrive  u64 [kGroupBarriers][W]   per-barrier arrival slots (a slot holding this call's
-//                                     epoch has arrived)
+//                                     token has arrived)
 //   counts  u64 [2][W]                epoch-tagged list lengths (tag44 << 20 | length)
 //   hist    u32 [kGroupCopies][256]   threshold histogram of the thread bests' high key byte,
 //                                     spread over kGroupCopies copies so that few workgroups
@@ -68,6 +73,22 @@ constexpr GroupLayout group_layout(int W) {
 // of an MI355X).
 constexpr int kMaxCoopGroups = 256;
 
+// Per-segment completion status (one u32 per segment in the workspace, written by every call;
+// RADIX_TOPK_STATUS_* of the C ABI).  A cross-workgroup wait is bounded: a workgroup that
+// gives up on one (its peers were not resident, or a test forced it) records kStatusTimeout
+// and fills its segment's row with the pad instead of hanging.
+constexpr uint32_t kStatusOk = 0;
+constexpr uint32_t kStatusTimeout = 1;
+// Polls of every bounded cross-workgroup wait (each poll is a device-coherent load and a
+// short sleep): about a second, far beyond any wait between co-resident workgroups.
+constexpr uint32_t kDefaultSpinLimit = 1u << 22;
+// Test hook bits (TopkParams::force_timeout): the named wait looks for a value nobody writes,
+// so it runs to its spin limit and takes the give-up path.
+constexpr uint32_t kForceFlagWait = 1;      // cooperative "histograms cleared" wait
+constexpr uint32_t kForceBarrier = 2;       // cooperative first barrier
+constexpr uint32_t kForceCollect = 4;       // cooperative list-length collection
+constexpr uint32_t kForcePairPoll = 8;      // two-chunk merger's poll for the published list
+
 // +inf bit patterns of the two 16-bit element formats; a magnitude above it is a NaN.
 constexpr uint32_t kInfBitsF16 = 0x7C00u;
 constexpr uint32_t kInfBitsBF16 = 0x7F80u;
@@ -107,6 +128,9 @@ struct TopkParams {
   float* probs;                 // [seg_num, k] or nullptr
   float inv_temperature;        // 1 / temperature, rounded to fp32
   unsigned char* groups;        // cooperative path: [seg_num] blocks of group_layout(W).bytes
+  uint32_t* status;             // [seg_num] completion status of this call (kStatus*)
+  uint32_t spin_limit;          // polls of every bounded cross-workgroup wait
+  uint32_t force_timeout;       // test hook: kForce* bits (0 in every ordinary call)
 };
 
 // One compiled instantiation of the fused kernel.

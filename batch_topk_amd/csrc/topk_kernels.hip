@@ -257,7 +257,7 @@ struct Smem {
   u32* hist;    // [256]
   u32* hist2;   // [256]
   int* scal;    // [32]
-  u32* wcnt;    // [16] (spare)
+  u32* wcnt;    // [16] (cooperative: words 0-1 hold the call token)
   u64* area;    // [kArea] contiguous candidate list
   u64* sel;     // [kpad]
   int* rank;    // [max(kpad, kRankCap)]
@@ -685,7 +685,8 @@ __device__ __forceinline__ void wait_vector_memory() { asm volatile("s_waitcnt v
 
 // Per-segment block of the cooperative path (layout in topk_common.hpp).
 struct GroupWs {
-  u64* flag;    // epoch-tagged "histograms cleared"
+  u64* flag;    // tagged "histograms cleared"
+  u64* gen;     // generation word: advanced once per call
   u64* arrive;  // [kGroupBarriers][W] arrival slots
   u64* counts;  // [2][W] epoch-tagged list lengths
   u32* hist;    // [kGroupCopies][256]
@@ -699,6 +700,7 @@ __device__ __forceinline__ GroupWs group_ws(const TopkParams& p, int seg) {
   unsigned char* b = p.groups + static_cast<size_t>(seg) * L.bytes;
   GroupWs g;
   g.flag = reinterpret_cast<u64*>(b + L.flag);
+  g.gen = g.flag + 1;
   g.arrive = reinterpret_cast<u64*>(b + L.arrive);
   g.counts = reinterpret_cast<u64*>(b + L.counts);
   g.hist = reinterpret_cast<u32*>(b + L.hist);
@@ -721,44 +723,59 @@ __device__ __forceinline__ void store_agent(u32* a, u32 v) {
   __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Epoch-tagged words (tag44 << 20 | value20): a word carrying another tag is stale (an
-// earlier call, or uninitialised workspace) and reads as "absent".
+// Tagged words (tag44 << 20 | value20): a word carrying another tag is stale (an earlier call,
+// or uninitialised workspace) and reads as "absent".
 constexpr u64 kTagMask = (1ull << 44) - 1;
 constexpr u32 kAbsent = 0xffffffffu;
+constexpr u32 kGaveUp = 0xfffffffeu;  // group_collect: a bounded wait gave up
 __device__ __forceinline__ u32 tagged_value(u64 word, u64 tag) {
   return (word >> 20) == tag ? static_cast<u32>(word & 0xfffffu) : kAbsent;
 }
 
-// Every bounded wait of the cooperative path: no wave may spin forever, even if the grid were
-// not co-resident (the launcher checks that it is).
-constexpr u32 kGroupSpinLimit = 1u << 22;
+// Token of one cooperative call: the host's call epoch (unique per call made from the host)
+// mixed with the segment block's generation word (advanced by every call, so unique per
+// replay of a captured call, whose epoch is frozen).  Its low 44 bits (the tag of tagged
+// words) are never zero, so a zeroed workspace holds no word of any call.
+__device__ __forceinline__ u64 call_token(u64 epoch, u64 gen) {
+  u64 t = epoch ^ (gen * 0x9E3779B97F4A7C15ull);
+  if ((t & kTagMask) == 0) t |= 1u;
+  return t;
+}
 
-// All `arrivals` workgroups of a segment meet here.  Each writes this call's epoch into its
+// All `arrivals` workgroups of a segment meet here.  Each writes this call's token into its
 // own arrival slot (no two workgroups touch one address), and threads 0..arrivals-1 each wait
-// for one slot.  Every thread first waits for its own cross-workgroup writes (agent-scope
-// atomics, device-coherent) to complete; after the barrier the workgroup's agent-scope loads
-// see every other workgroup's writes.
-__device__ __forceinline__ void group_barrier(u64* slots, u64 epoch, int w, int arrivals) {
+// for one slot to hold `expect` (the token; anything else only under the test hook).  Every
+// thread first waits for its own cross-workgroup writes (agent-scope atomics,
+// device-coherent) to complete; after the barrier the workgroup's agent-scope loads see every
+// other workgroup's writes.  Each wait is bounded by `limit` polls; returns false
+// (workgroup-uniform) when one gave up.
+__device__ __forceinline__ bool group_barrier(u64* slots, u64 token, u64 expect, int w, int arrivals,
+                                              u32 limit) {
   wait_vector_memory();
   __syncthreads();
   const int tid = threadIdx.x;
-  if (tid == 0) store_agent(slots + w, epoch);
+  if (tid == 0) store_agent(slots + w, token);
+  int late = 0;
   if (tid < arrivals) {
-    for (u32 spin = 0; spin < kGroupSpinLimit; ++spin) {
-      if (load_agent(slots + tid) == epoch) break;
+    late = 1;
+    for (u32 spin = 0; spin < limit; ++spin) {
+      if (load_agent(slots + tid) == expect) {
+        late = 0;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
   }
-  __syncthreads();
+  return __syncthreads_or(late) == 0;
 }
 
 // Threshold histogram of the whole segment: every workgroup adds its LDS histogram to copy
 // (w mod kGroupCopies) of the global one (nonzero bins only), the workgroups meet, and each
 // loads the sum of the copies back into LDS (four copies per thread, partial sums staged in
-// `scratch`, 1024 words of LDS).
+// `scratch`, 1024 words of LDS).  Returns false when the meeting gave up.
 template <int BLOCK>
-__device__ void group_histogram(u32* lds_hist, u32* ghist, u32* scratch, u64* slots, u64 epoch, int w,
-                                int arrivals) {
+__device__ bool group_histogram(u32* lds_hist, u32* ghist, u32* scratch, u64* slots, u64 token,
+                                u64 expect, int w, int arrivals, u32 limit) {
   constexpr int Q = BLOCK / 256;  // threads per bin in the copy sum
   static_assert(Q >= 1 && kGroupCopies % Q == 0, "the copy sum splits the copies over Q threads per bin");
   const int tid = threadIdx.x;
@@ -769,7 +786,7 @@ __device__ void group_histogram(u32* lds_hist, u32* ghist, u32* scratch, u64* sl
                              __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  group_barrier(slots, epoch, w, arrivals);
+  if (!group_barrier(slots, token, expect, w, arrivals, limit)) return false;
   const int bin = tid & 255;
   const int q = tid >> 8;
   u32 part = 0;
@@ -784,46 +801,51 @@ __device__ void group_histogram(u32* lds_hist, u32* ghist, u32* scratch, u64* sl
     lds_hist[tid] = sum;
   }
   __syncthreads();
+  return true;
 }
 
-// Single-copy variant for the (rare) refinement digits.
+// Single-copy variant for the (rare) refinement digits.  Returns false when the meeting gave up.
 template <int BLOCK>
-__device__ void group_histogram_single(u32* lds_hist, u32* ghist, u64* slots, u64 epoch, int w,
-                                       int arrivals) {
+__device__ bool group_histogram_single(u32* lds_hist, u32* ghist, u64* slots, u64 token, int w,
+                                       int arrivals, u32 limit) {
   const int tid = threadIdx.x;
   if (tid < 256) {
     const u32 c = lds_hist[tid];
     if (c) __hip_atomic_fetch_add(ghist + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  group_barrier(slots, epoch, w, arrivals);
+  if (!group_barrier(slots, token, token, w, arrivals, limit)) return false;
   if (tid < 256) lds_hist[tid] = load_agent(ghist + tid);
   __syncthreads();
+  return true;
 }
 
 // Whole-segment candidate list from the workgroups' lists.  Each workgroup has stored its
-// list and then, as its arrival, its epoch-tagged length: threads 0..arrivals-1 each wait for
-// one length (no separate barrier), wave 0 prefix-sums them, and if no list overflowed and
-// the total fits kGroupCap every entry is gathered into `area`.  Returns the total, or
-// kAbsent when the list cannot be formed.  `cnt` and `pre` are 256-int LDS arrays.
+// list and then, as its arrival, its tagged length: threads 0..arrivals-1 each wait for one
+// length (no separate barrier), wave 0 prefix-sums them, and if no list overflowed and the
+// total fits kGroupCap every entry is gathered into `area`.  Returns the total, kAbsent when
+// the list cannot be formed, or kGaveUp when a wait for a length gave up (after `limit` polls;
+// `want` is the tag of this call's lengths).  `cnt` and `pre` are 256-int LDS arrays.
 template <int BLOCK>
-__device__ u32 group_collect(const u64* counts, const u64* lists, u64 tag, int arrivals, u64* area,
-                             int* cnt, int* pre, int* scal) {
+__device__ u32 group_collect(const u64* counts, const u64* lists, u64 want, int arrivals, u64* area,
+                             int* cnt, int* pre, int* scal, u32 limit) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  int late = 0;
   if (tid < 256) {
     u32 c = 0;
     if (tid < arrivals) {
       c = kAbsent;
-      for (u32 spin = 0; spin < kGroupSpinLimit; ++spin) {
-        c = tagged_value(load_agent(counts + tid), tag);
+      for (u32 spin = 0; spin < limit; ++spin) {
+        c = tagged_value(load_agent(counts + tid), want);
         if (c != kAbsent) break;
         __builtin_amdgcn_s_sleep(1);
       }
-      if (c > static_cast<u32>(kCandArea)) c = static_cast<u32>(kGroupCap) + 1u;  // overflow or absent
+      late = c == kAbsent ? 1 : 0;
+      if (c > static_cast<u32>(kCandArea)) c = static_cast<u32>(kGroupCap) + 1u;  // overflow
     }
     cnt[tid] = static_cast<int>(c);
   }
-  __syncthreads();
+  if (__syncthreads_or(late)) return kGaveUp;
   if (tid < 64) {
     const int c0 = cnt[4 * lane], c1 = cnt[4 * lane + 1], c2 = cnt[4 * lane + 2], c3 = cnt[4 * lane + 3];
     const u32 sum = static_cast<u32>(c0 + c1 + c2 + c3);
@@ -887,6 +909,20 @@ __device__ void rank_range_write(const TopkParams& p, int64_t n, int seg, const 
     for (int j = lane; j < M; j += 64) c += list[j] < P ? 1u : 0u;
     const u32 r = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_scan(c)), 63));
     if (lane == 0 && r < static_cast<u32>(kk)) write_rank<E>(p, n, seg, static_cast<int>(r), P);
+  }
+}
+
+// A bounded cross-workgroup wait gave up: the workgroup fills its segment's row with the pad,
+// records the timeout in the segment's status word (which the call reset before any of its
+// workgroups could give up) and advances the segment block's generation word, if it has one,
+// so the next call on this workspace uses a token no workgroup of this call has used.  The
+// caller then returns without writing any other cross-workgroup word.
+template <int BLOCK, class E>
+__device__ void give_up_row(const TopkParams& p, int seg, u64* gen) {
+  for (int r = threadIdx.x; r < p.k; r += BLOCK) write_pad<E>(p, static_cast<int64_t>(seg) * p.k + r);
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_or(p.status + seg, kStatusTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (gen) __hip_atomic_fetch_add(gen, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -967,6 +1003,7 @@ segmented_topk_kernel(TopkParams p) {
         const int64_t o = static_cast<int64_t>(seg) * k + r;
         write_pad<E>(p, o);
       }
+      if (tid == 0) store_agent(p.status + seg, kStatusOk);
       if constexpr (!COOP && E::kBytes == 2) {
         if (p.samples) sample_segment(p, nullptr, 0, seg);
       }
@@ -975,6 +1012,9 @@ segmented_topk_kernel(TopkParams p) {
   }
   const int Ws = static_cast<int>(Ws64);
   if (w >= Ws) return;
+  // A segment of one chunk has no cross-workgroup wait: it completes.  (Multi-chunk segments
+  // record their status where they merge, or, cooperatively, at the start.)
+  if (!COOP && Ws == 1 && tid == 0) p.status[seg] = kStatusOk;
 
   const int kk = n < k ? static_cast<int>(n) : k;
   // A two-chunk segment merges through one published list (step 5).
@@ -989,20 +1029,29 @@ segmented_topk_kernel(TopkParams p) {
   const u32 idx_base = static_cast<u32>(cb - s0);  // segment index = idx_base + position
   const int need = COOP ? kk : kc;  // rank the threshold must cover (segment or chunk)
 
-  // Cooperative path: workgroup 0 clears the segment's global histograms of this call before
-  // loading its chunk, then raises the epoch-tagged "cleared" flag.
+  // Cooperative path: every workgroup reads the segment block's generation word and derives
+  // the call token from it (thread 0, broadcast through LDS at the barrier below).  Workgroup 0
+  // resets the segment's status, clears the segment's global histograms of this call before
+  // loading its chunk, then raises the tagged "cleared" flag; once every workgroup has passed
+  // the first barrier (and so has read the generation), it advances the generation for the
+  // next call.
   const u64 epoch = p.epoch;
-  const u64 tag = epoch & kTagMask;
+  u64 token = epoch;  // cooperative: this call's token (thread 0 until the broadcast)
   GroupWs g{};
   if constexpr (COOP) {
     g = group_ws(p, seg);
+    if (tid == 0) {
+      token = call_token(epoch, load_agent(g.gen));
+      reinterpret_cast<u64*>(sm.wcnt)[0] = token;
+      if (w == 0) store_agent(p.status + seg, kStatusOk);
+    }
     if (w == 0) {
       for (int i = tid; i < kGroupCopies * 256; i += BLOCK) store_agent(g.hist + i, 0u);
       for (int i = tid; i < kFineCopies * kFineBins; i += BLOCK) store_agent(g.fine + i, 0u);
       for (int i = tid; i < kRefineDigits * 256; i += BLOCK) store_agent(g.rhist + i, 0u);
       wait_vector_memory();
       __syncthreads();
-      if (tid == 0) store_agent(g.flag, (tag << 20) | 1u);
+      if (tid == 0) store_agent(g.flag, ((token & kTagMask) << 20) | 1u);
     }
   }
 
@@ -1040,6 +1089,8 @@ segmented_topk_kernel(TopkParams p) {
     for (int i = tid; i < kFineBins; i += BLOCK) fine[i] = 0;
   }
   __syncthreads();  // histograms cleared (the loads stay in flight)
+  if constexpr (COOP) token = reinterpret_cast<const u64*>(sm.wcnt)[0];
+  const u64 tag = token & kTagMask;
   TOPK_TRACE(12);
   // Positions outside [lo, hi) become the filler.  lo > 0 only in a segment's first chunk,
   // where it is below 8, so only vector 0 can start before lo; whether a vector index reaches
@@ -1138,13 +1189,22 @@ segmented_topk_kernel(TopkParams p) {
     u32* fine = reinterpret_cast<u32*>(sm.area);
     atomicAdd(&fine[best_key >> 5], 1u);
     __syncthreads();
+    int late = 0;
     if (tid == 0) {  // the global histograms are cleared
-      for (u32 spin = 0; spin < kGroupSpinLimit; ++spin) {
-        if (tagged_value(load_agent(g.flag), tag) == 1u) break;
+      const u32 want = (p.force_timeout & kForceFlagWait) ? 2u : 1u;
+      late = 1;
+      for (u32 spin = 0; spin < p.spin_limit; ++spin) {
+        if (tagged_value(load_agent(g.flag), tag) == want) {
+          late = 0;
+          break;
+        }
         __builtin_amdgcn_s_sleep(1);
       }
     }
-    __syncthreads();
+    if (__syncthreads_or(late)) {
+      give_up_row<BLOCK, E>(p, seg, g.gen);
+      return;
+    }
     // this workgroup's nonzero fine bins into its copy; the coarse ones go in group_histogram
     for (int i = tid; i < kFineBins; i += BLOCK) {
       const u32 c = fine[i];
@@ -1153,7 +1213,13 @@ segmented_topk_kernel(TopkParams p) {
                                __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    group_histogram<BLOCK>(sm.hist, g.hist, sm.stage, g.arrive, epoch, w, Ws);
+    const u64 expect = (p.force_timeout & kForceBarrier) ? (token ^ 1u) : token;
+    if (!group_histogram<BLOCK>(sm.hist, g.hist, sm.stage, g.arrive, token, expect, w, Ws, p.spin_limit)) {
+      give_up_row<BLOCK, E>(p, seg, g.gen);
+      return;
+    }
+    // Every workgroup has read the generation word: advance it for the next call.
+    if (w == 0 && tid == 0) __hip_atomic_fetch_add(g.gen, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     TOPK_TRACE(8);
     if (wid == 0) wave_find_bucket(sm.hist, need, sm.scal + 8, lane);
     __syncthreads();
@@ -1403,7 +1469,12 @@ segmented_topk_kernel(TopkParams p) {
     __syncthreads();
     if (tid == 0) store_agent(g.counts + w, (tag << 20) | contrib);
     TOPK_TRACE(10);
-    u32 total = group_collect<BLOCK>(g.counts, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20);
+    const u64 want = (p.force_timeout & kForceCollect) ? (tag ^ 1u) : tag;
+    u32 total = group_collect<BLOCK>(g.counts, g.lists, want, Ws, sm.area, cnt, pre, sm.scal + 20, p.spin_limit);
+    if (total == kGaveUp) {
+      give_up_row<BLOCK, E>(p, seg, g.gen);
+      return;
+    }
     if (total == kAbsent) {
       // ---- 4d. the list would not fit: exact radix refinement over the whole segment of
       // Q = key << 32 | index32 among the elements with key prefix <= T, one global histogram
@@ -1422,7 +1493,11 @@ segmented_topk_kernel(TopkParams p) {
           if (E::prefix(b, inf) <= T && (Q & pmask) == prefix) atomicAdd(&sm.hist[(Q >> shift) & 255u], 1u);
         });
         __syncthreads();
-        group_histogram_single<BLOCK>(sm.hist, g.rhist + pass * 256, g.arrive + (3 + pass) * W, epoch, w, Ws);
+        if (!group_histogram_single<BLOCK>(sm.hist, g.rhist + pass * 256, g.arrive + (3 + pass) * W, token, w,
+                                           Ws, p.spin_limit)) {
+          give_up_row<BLOCK, E>(p, seg, g.gen);
+          return;
+        }
         if (wid == 0) wave_find_bucket(sm.hist, rneed, sm.scal, lane);
         __syncthreads();
         const int b = sm.scal[0];
@@ -1451,7 +1526,11 @@ segmented_topk_kernel(TopkParams p) {
       wait_vector_memory();
       __syncthreads();
       if (tid == 0) store_agent(g.counts + W + w, (tag << 20) | c2);
-      total = group_collect<BLOCK>(g.counts + W, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20);
+      total = group_collect<BLOCK>(g.counts + W, g.lists, tag, Ws, sm.area, cnt, pre, sm.scal + 20, p.spin_limit);
+      if (total == kGaveUp) {
+        give_up_row<BLOCK, E>(p, seg, g.gen);
+        return;
+      }
       if (total == kAbsent) total = 0;  // cannot happen: at most kCandArea elements are <= bound
     }
     // Every workgroup ranks its share of the list; workgroup 0 writes the pads.
@@ -1577,6 +1656,7 @@ segmented_topk_kernel(TopkParams p) {
       u64* ol = p.lists + other * p.cap_list;
       u32* oc = reinterpret_cast<u32*>(p.list_counts) + other;
       const int cap = p.cap_list;
+      const u32 want = (p.force_timeout & kForcePairPoll) ? (ctag ^ 1u) : ctag;
       int mp = 0;
       int seen = 0;  // workgroup-uniform count of waves that found a stale word so far
       u32 spin = 0;
@@ -1585,7 +1665,7 @@ segmented_topk_kernel(TopkParams p) {
         const u64 x = tid < cap ? load_agent(ol + tid) : 0ull;
         mp = static_cast<int>(h & 0xffffu);
         mp = mp < cap ? mp : cap;
-        const bool bad = (h >> 16) != ctag || (tid < mp && (x & kPairTagMask) != etag);
+        const bool bad = (h >> 16) != want || (tid < mp && (x & kPairTagMask) != etag);
         if (ballot(bad) && lane == 0) atomicAdd(&sm.scal[6], 1);
         __syncthreads();
         const int now = sm.scal[6];
@@ -1594,19 +1674,24 @@ segmented_topk_kernel(TopkParams p) {
           break;
         }
         seen = now;
-        if (spin >= kGroupSpinLimit) {  // the publisher never arrived: cannot happen
-          mp = 0;
+        if (spin >= p.spin_limit) {  // gave up (the publisher has started, so only the test hook)
+          mp = -1;
           break;
         }
         __syncthreads();  // every wave has read the count before the next round adds to it
         __builtin_amdgcn_s_sleep(1);
       }
       TOPK_TRACE_VALUE(13, spin + 1);
-      if (tid < mp) store_agent(ol + tid, 0ull);
+      if (tid < (mp < 0 ? cap : mp)) store_agent(ol + tid, 0ull);
       if (tid == 0) {
         store_agent(oc, 0u);
         store_agent(p.tickets + seg, 0ull);
       }
+      if (mp < 0) {
+        give_up_row<BLOCK, E>(p, seg, nullptr);
+        return;
+      }
+      if (tid == 0) p.status[seg] = kStatusOk;
       Mf = M + mp;
     } else {
       // Three or more chunks: every workgroup publishes, the last to arrive merges.
@@ -1623,6 +1708,7 @@ segmented_topk_kernel(TopkParams p) {
       __syncthreads();
       TOPK_TRACE(9);
       if (!sm.scal[5]) return;
+      if (tid == 0) p.status[seg] = kStatusOk;
 
       int total = 0;
       for (int c = 0; c < Ws; ++c) {

@@ -128,6 +128,35 @@ def run_floor(calls: int) -> None:
         torch.cuda.synchronize()
         us = a.elapsed_time(b) * 1e3 / calls
         print(f"{w} | {block} x {vpt} | {us:.2f} | {nbytes / us / 1e3:.0f} | {nbytes / us / 1e3 / 8000:.3f}")
+    # Asymptotic streaming rate: the same loads over 512 MiB per launch (2048 rows of 131,072
+    # fp16, two buffers alternating), where the launch cost and the ramp are a few percent.
+    big_rows, big_len = 2048, 131072
+    big = [torch.empty(big_rows * big_len, dtype=torch.int16, device="cuda:0") for _ in range(2)]
+    for t in big:
+        t.fill_(1)
+    big_calls = 40
+    bptrs = (ctypes.c_void_p * big_calls)(*[big[i % 2].data_ptr() for i in range(big_calls)])
+    bout = torch.empty(big_rows * 4 * 16, dtype=torch.int32, device="cuda:0")
+    big_bytes = 2 * big_rows * big_len
+    print(f"streaming read of {big_rows} x {big_len} fp16 ({big_bytes} bytes) per launch, "
+          f"{big_calls} back-to-back launches over 2 buffers")
+    print("workgroups per row | threads x vectors | us per launch | GB/s | fraction of 8 TB/s")
+    for block, vpt, w in ((1024, 16, 1), (512, 16, 2), (256, 16, 4)):
+        def go_big():
+            rc = lib.read_floor_run(bptrs, big_calls, big_rows, big_len, block, vpt, w, bout.data_ptr(),
+                                    stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"read_floor_run returned {rc}")
+        go_big()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        go_big()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / big_calls
+        print(f"{w} | {block} x {vpt} | {us:.2f} | {big_bytes / us / 1e3:.0f} | "
+              f"{big_bytes / us / 1e3 / 8000:.3f}")
 
 
 PHASES = ((12, "loads issued"), (1, "thread best"), (2, "first histogram round"),

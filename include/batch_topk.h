@@ -190,6 +190,41 @@ int radix_topk_batch_topk_ex(const void* d_input, int format, const int32_t* d_o
 size_t radix_topk_batch_topk_ex_workspace_size(int format, int segmented, int seg_num, int seg_len,
                                                int k);
 
+/* Per-segment completion status of a call (radix_topk_workspace_status). */
+#define RADIX_TOPK_STATUS_OK 0
+#define RADIX_TOPK_STATUS_WAIT_TIMEOUT 1
+
+/*
+ * Completion status of the last call made with this workspace, one word per segment, copied
+ * to the host array h_status[seg_num] (seg_num as in that call).  The call synchronises
+ * `stream`, on which the top-k call must have been issued (or a stream ordered after it).
+ *   RADIX_TOPK_STATUS_OK: the segment's row was written completely.
+ *   RADIX_TOPK_STATUS_WAIT_TIMEOUT: a workgroup of the segment gave up a bounded wait for
+ *   another workgroup of the same call (the segment's workgroups were not all resident at
+ *   once, e.g. because kernels of other streams or processes held the GPU's compute units);
+ *   the row holds the pad (index -1, value bits all ones) in some or all ranks.
+ * Segments split over several workgroups wait for each other: long segments with large k run
+ * as one grid whose workgroups must all be resident at once.  Every such wait is bounded, so
+ * the kernel always finishes; this query tells a caller whether the rows are complete.
+ * Every call rewrites every segment's word, so a call after a timed-out one reports its own
+ * status.  Returns 0, 1 (NULL pointers, seg_num <= 0, workspace too small for seg_num
+ * segments) or the HIP error of the copy.
+ * No counterpart in the reference, whose chain of kernel launches never waits across
+ * workgroups (reference src/batch_topk.cu:42-193).
+ */
+int radix_topk_workspace_status(const void* d_workspace, size_t workspace_bytes, int seg_num,
+                                uint32_t* h_status, void* stream);
+
+/*
+ * Test hook, not for production use: every later call bounds each cross-workgroup wait at
+ * spin_limit polls and, for every bit of force_mask (1: the long-segment grid's first wait,
+ * 2: its first meeting, 4: its list collection, 8: the two-chunk merge), makes that wait look
+ * for a value no workgroup writes, so it times out, fills the segment's row with the pad and
+ * reports RADIX_TOPK_STATUS_WAIT_TIMEOUT, with every kernel still running to its end.
+ * spin_limit = 0 restores ordinary calls.  Process-wide; not synchronised with calls in flight.
+ */
+void radix_topk_debug_wait_hook(uint32_t spin_limit, uint32_t force_mask);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -149,9 +149,10 @@ def test_f32_ex_flags_and_torch_mirror():
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(21)
     bits = _bits(3, rng, 64 * 20000).reshape(64, 20000)
-    plain = run_f32(bits, 256)
+    plain = O.batch_topk_half(bits, 256, seg_len=20000, threads=THREADS, fmt="f32")
+    assert_same(run_f32(bits, 256), plain, "f32 plain entry point vs oracle")
     announce("f32 ex flags")
-    assert_same(run_f32(bits, 256, flags=0), plain, "f32 ex flags=0")
+    assert_same(run_f32(bits, 256, flags=0), plain, "f32 ex flags=0 vs oracle")
     v, i = run_f32(bits, 256, flags=bt.UNSORTED)
     for r in range(64):
         o, e = np.argsort(i[r]), np.argsort(plain[1][r])

@@ -20,7 +20,7 @@ P_IN, P_VAL, P_IDX, P_WS, P_OFF = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
 def declared_symbols():
     with open(os.path.join(ROOT, "include", "batch_topk.h")) as f:
         text = f.read()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(radix_topk_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|void)\s+(radix_topk_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():

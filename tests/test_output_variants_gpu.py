@@ -1,9 +1,9 @@
 """GPU parity of radix_topk_batch_topk_ex: every layout, format and output flag against the
-plain entry points (themselves checked against the oracle).
+oracle (and the plain entry points against the same oracle rows).
 
-flags = 0 must give the plain results bit for bit; UNSORTED must give, in each row's first
-min(k, length) slots, the same set of (index, value bits) entries, and the pad after them;
-INDICES_ONLY must give the same indices and leave the value array untouched."""
+flags = 0 must give the oracle's rows bit for bit; UNSORTED must give, in each row's first
+min(k, length) slots, the oracle row's set of (index, value bits) entries, and the pad after
+them; INDICES_ONLY must give the oracle's indices and leave the value array untouched."""
 
 import numpy as np
 import pytest
@@ -54,17 +54,21 @@ def run_ex(bits, k, flags, fmt=bt.FORMAT_F16, offsets=None, max_len=None):
 def check_variants(bits, k, what, fmt=bt.FORMAT_F16, offsets=None, max_len=None):
     fmt_name = "f16" if fmt == bt.FORMAT_F16 else "bf16"
     if offsets is None:
+        exp = O.batch_topk_half(bits, k, seg_len=bits.shape[1], threads=THREADS, fmt=fmt_name)
         plain = run_fixed(bits, k, fmt=fmt_name)
         lengths = np.full(bits.shape[0], bits.shape[1])
     else:
+        exp = O.batch_topk_half(bits, k, offsets=offsets.astype(np.int64), threads=THREADS, fmt=fmt_name)
         plain = run_segmented(bits, offsets, k, max_len, fmt=fmt_name)
         lengths = np.diff(offsets)
+    ev, ei = exp  # ranks past a segment's length hold the pad, as the entry points write it
+    assert_same(plain, (ev, ei), f"{what} plain entry point vs oracle")
     announce(f"ex flags=0 {what}")
-    assert_same(run_ex(bits, k, 0, fmt, offsets, max_len), plain, f"{what} flags=0")
+    assert_same(run_ex(bits, k, 0, fmt, offsets, max_len), (ev, ei), f"{what} flags=0 vs oracle")
 
     announce(f"ex indices only {what}")
     v, i = run_ex(bits, k, bt.INDICES_ONLY, fmt, offsets, max_len)
-    assert np.array_equal(i, plain[1]), f"{what} indices only"
+    assert np.array_equal(i, ei), f"{what} indices only vs oracle"
     assert np.all(v == SENTINEL), f"{what}: values written by an indices-only call"
 
     for flags in (bt.UNSORTED, bt.UNSORTED | bt.INDICES_ONLY):
@@ -74,13 +78,13 @@ def check_variants(bits, k, what, fmt=bt.FORMAT_F16, offsets=None, max_len=None)
             m = int(min(k, lengths[r]))
             got_i = i[r, :m]
             order = np.argsort(got_i, kind="stable")
-            exp_order = np.argsort(plain[1][r, :m], kind="stable")
-            assert np.array_equal(got_i[order], plain[1][r, :m][exp_order]), (what, flags, r)
+            exp_order = np.argsort(ei[r, :m], kind="stable")
+            assert np.array_equal(got_i[order], ei[r, :m][exp_order]), (what, flags, r)
             assert np.all(i[r, m:] == -1), (what, flags, r)
             if flags & bt.INDICES_ONLY:
                 assert np.all(v[r] == SENTINEL), (what, flags, r)
             else:
-                assert np.array_equal(v[r, :m][order], plain[0][r, :m][exp_order]), (what, flags, r)
+                assert np.array_equal(v[r, :m][order], ev[r, :m][exp_order]), (what, flags, r)
                 assert np.all(v[r, m:] == 0xFFFF), (what, flags, r)
 
 
@@ -124,8 +128,6 @@ def test_ex_segmented_and_bf16_variants():
     f32 = rng.standard_normal((64, 20000)).astype(np.float32)
     bf = (f32.view(np.uint32) >> 16).astype(np.uint16)
     check_variants(bf, 256, "bf16 64x20000 k=256", fmt=bt.FORMAT_BF16)
-    exp = O.batch_topk_half(bf, 256, seg_len=20000, threads=THREADS, fmt="bf16")
-    assert_same(run_ex(bf, 256, 0, bt.FORMAT_BF16), exp, "bf16 ex vs oracle")
 
 
 def test_torch_mirror_sorted_and_values_options():
@@ -138,6 +140,9 @@ def test_torch_mirror_sorted_and_values_options():
     vu, iu = bt.topk(x, 200, sorted=False)
     vn, inn = bt.topk(x, 200, values=False)
     torch.cuda.synchronize()
+    ev, ei = O.batch_topk_half(bits.view(np.uint16), 200, seg_len=30000, threads=THREADS)
+    assert np.array_equal(i.cpu().numpy(), ei)
+    assert np.array_equal(v.view(torch.int16).cpu().numpy().view(np.uint16), ev)
     assert vn is None and torch.equal(inn, i)
     si, order = torch.sort(iu.long(), dim=1)
     se, order_e = torch.sort(i.long(), dim=1)
