@@ -21,6 +21,11 @@ SOURCES = ["topk_kernels.hip", "sample_kernels.hip", "api.cpp"]
 # batch_topk_amd/profiling.py only.
 FLOOR_LIB_PATH = os.path.join(HERE, "libread_floor.so")
 FLOOR_SOURCES = ["read_floor.hip"]
+# A C++ caller of the reference's host API compiled against include/batch_topk.hpp and linked
+# against the engine (run by tests/test_cpp_dropin_gpu.py).
+ROOT = os.path.dirname(HERE)
+CPP_CALLER_SRC = os.path.join(ROOT, "tests", "cpp", "dropin_caller.cpp")
+CPP_CALLER_BIN = os.path.join(ROOT, "tests", "cpp", "dropin_caller")
 # Measurement build of the engine with the per-phase clock stamps compiled in
 # (-DTOPK_PHASE_TRACE): loaded by batch_topk_amd/profiling.py only, never by the package.
 TRACE_LIB_PATH = os.path.join(HERE, "libbatch_topk_amd_trace.so")
@@ -53,12 +58,28 @@ def _compile(sources, out_path: str, verbose: bool, defines=()) -> None:
     os.replace(tmp, out_path)
 
 
+def build_cpp_caller(verbose: bool = False) -> str:
+    """The drop-in C++ caller (host code only), linked against the in-tree engine library."""
+    tmp = CPP_CALLER_BIN + ".tmp"
+    cmd = [hipcc(), "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), "-o", tmp,
+           CPP_CALLER_SRC, "-L", HERE, "-lbatch_topk_amd", "-Wl,-rpath,$ORIGIN/../../batch_topk_amd"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed to build the drop-in C++ caller")
+    os.replace(tmp, CPP_CALLER_BIN)
+    return CPP_CALLER_BIN
+
+
 def build(verbose: bool = False) -> str:
-    """Always recompiles (the build check must exercise the compiler): the engine library and
-    the two measurement libraries (read floor, phase-traced engine)."""
+    """Always recompiles (the build check must exercise the compiler): the engine library, the
+    two measurement libraries (read floor, phase-traced engine) and the drop-in C++ caller."""
     _compile(SOURCES, LIB_PATH, verbose)
     _compile(FLOOR_SOURCES, FLOOR_LIB_PATH, verbose)
     _compile(SOURCES, TRACE_LIB_PATH, verbose, defines=("TOPK_PHASE_TRACE",))
+    build_cpp_caller(verbose)
     return LIB_PATH
 
 

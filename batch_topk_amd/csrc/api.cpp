@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cmath>
@@ -84,20 +85,36 @@ Plan make_plan(int seg_num, int64_t max_len, int k, int ev = 8, bool shared_alig
       if (found) break;
     }
   }
-  const int chunk = block * vpt * ev;
-  const int64_t W = span <= chunk ? 1 : (span + chunk - 1) / chunk;
+  int chunk = block * vpt * ev;
+  int64_t W = span <= chunk ? 1 : (span + chunk - 1) / chunk;
   const int kpad = next_pow2(k < 64 ? 64 : k);
   int cap_list = W > 1 ? next_pow2(2 * k > 128 ? 2 * k : 128) : 0;
   bool cooperative = false;
+  int group = 0;
   if (W > 1 && W * static_cast<int64_t>(cap_list) > kCandArea) {
-    // Too many lists to merge in LDS: cooperative path, if the grid can be co-resident.  The
-    // workspace covers the worst-case misalignment (W chunks).  Rows of a shared alignment
-    // launch with their exact chunk count, ceil(max_len / chunk) when 16-byte aligned (a
-    // misaligned pointer that needs more co-resident workgroups is refused at launch).
-    const int64_t w_launch = shared_alignment ? (max_len + chunk - 1) / chunk : W;
-    if (static_cast<int64_t>(seg_num) * w_launch > kMaxCoopGroups) return plan;
-    cooperative = true;
+    // Too many lists to merge in LDS: one whole-segment threshold, over chunks of 1024 threads x
+    // 16 vectors (a segment that then fits one chunk is a plain single-chunk row).
+    block = 1024;
+    vpt = 16;
+    chunk = block * vpt * ev;
+    W = span <= chunk ? 1 : (span + chunk - 1) / chunk;
     cap_list = 0;
+    if (W > 1) {
+      // The cooperative path (one workgroup per chunk, all co-resident) when the grid fits the
+      // CUs.  The workspace covers the worst-case misalignment (W chunks).  Rows of a shared
+      // alignment launch with their exact chunk count, ceil(max_len / chunk) when 16-byte
+      // aligned (a misaligned pointer that needs more co-resident workgroups is refused at
+      // launch).
+      const int64_t w_launch = shared_alignment ? (max_len + chunk - 1) / chunk : W;
+      if (static_cast<int64_t>(seg_num) * w_launch <= kMaxCoopGroups) {
+        cooperative = true;
+      } else {
+        // The long-segment path: `group` workgroups per segment, each taking every group-th
+        // chunk of it, as many per segment as the CUs hold at once for few segments, one per
+        // segment (no waiting across workgroups) otherwise.
+        group = seg_num <= kMaxCoopGroups ? static_cast<int>(std::min<int64_t>(W, kMaxCoopGroups / seg_num)) : 1;
+      }
+    }
   }
   if (static_cast<int64_t>(seg_num) * W > 0x7fffffff) return plan;
 
@@ -113,11 +130,15 @@ Plan make_plan(int seg_num, int64_t max_len, int k, int ev = 8, bool shared_alig
                    static_cast<size_t>(kpad) * 8 + static_cast<size_t>(rank_cap) * 4 +
                    static_cast<size_t>(block / 64) * kStageWords * 4;
   plan.cooperative = cooperative;
+  plan.group = group;
   size_t ws = kAlign;                                        // alignment slack of the carve
   ws += align_up(static_cast<size_t>(seg_num) * 8, kAlign);  // arrival tickets
   ws += align_up(static_cast<size_t>(seg_num) * 4, kAlign);  // per-segment status words
   if (cooperative) {
     ws += static_cast<size_t>(seg_num) * group_layout(static_cast<int>(W)).bytes;  // group blocks
+  } else if (group > 1) {
+    // (one workgroup per segment keeps its histograms and list in LDS: no block)
+    ws += static_cast<size_t>(seg_num) * group_layout(group).bytes;
   } else if (W > 1) {
     ws += align_up(static_cast<size_t>(seg_num) * W * 4, kAlign);               // list counts
     ws += static_cast<size_t>(seg_num) * W * static_cast<size_t>(cap_list) * 8;  // lists
@@ -202,7 +223,8 @@ int run(const Plan& plan, uint32_t inf_bits, const void* d_input, const int32_t*
   p.status = reinterpret_cast<uint32_t*>(ws + off);
   off += align_up(static_cast<size_t>(seg_num) * 4, kAlign);
   p.cooperative = plan.cooperative ? 1 : 0;
-  if (plan.cooperative) {
+  p.group = plan.group;
+  if (plan.cooperative || plan.group > 0) {
     p.groups = reinterpret_cast<unsigned char*>(ws + off);
   } else if (plan.W > 1) {
     p.list_counts = reinterpret_cast<int32_t*>(ws + off);
@@ -214,16 +236,18 @@ int run(const Plan& plan, uint32_t inf_bits, const void* d_input, const int32_t*
   const uint64_t hook = g_wait_hook.load(std::memory_order_relaxed);
   p.spin_limit = hook ? static_cast<uint32_t>(hook >> 32) : kDefaultSpinLimit;
   p.force_timeout = static_cast<uint32_t>(hook);
-  // Sampling is fused into the kernel's last step, except on a cooperative plan (the ranking
-  // is spread over the segment's workgroups): there a one-wave-per-row kernel follows.
-  if (sample && !plan.cooperative) {
+  // Sampling is fused into the kernel's last step, except on the whole-segment plans
+  // (cooperative or long-segment: the ranking is spread over the segment's workgroups): there a
+  // one-wave-per-row kernel follows.
+  const bool whole_segment = plan.cooperative || plan.group > 0;
+  if (sample && !whole_segment) {
     p.uniforms = sample->uniforms;
     p.samples = sample->samples;
     p.probs = sample->probs;
     p.inv_temperature = sample->inv_temperature;
   }
   const int rc = launch_segmented_topk(plan, p, stream);
-  if (rc != 0 || !sample || !plan.cooperative) return rc;
+  if (rc != 0 || !sample || !whole_segment) return rc;
   SampleParams sp{};
   sp.topk_vals = static_cast<const uint16_t*>(d_values);
   sp.topk_idx = d_indices;

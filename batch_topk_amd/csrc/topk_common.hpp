@@ -128,6 +128,8 @@ struct TopkParams {
   float* probs;                 // [seg_num, k] or nullptr
   float inv_temperature;        // 1 / temperature, rounded to fp32
   unsigned char* groups;        // cooperative path: [seg_num] blocks of group_layout(W).bytes
+  int32_t group;                // long-segment path: workgroups per segment (each takes every
+                                //   group-th chunk of it), 0 on every other path
   uint32_t* status;             // [seg_num] completion status of this call (kStatus*)
   uint32_t spin_limit;          // polls of every bounded cross-workgroup wait
   uint32_t force_timeout;       // test hook: kForce* bits (0 in every ordinary call)
@@ -151,6 +153,8 @@ struct Plan {
   size_t lds_bytes;
   size_t ws_bytes;  // workspace bytes (includes 256 bytes of alignment slack)
   bool cooperative; // all W workgroups of a segment co-resident, one shared threshold
+  int group;        // long-segment path (> 0): workgroups per segment, each taking several
+                    // chunks; the grid is seg_num * group (co-resident when group > 1)
   bool ok;
 };
 

@@ -234,22 +234,6 @@ __device__ __forceinline__ u32 wave_inclusive_scan(u32 x) {
   return x;
 }
 
-// Ascending bitonic sort of one u64 per lane across a wave64.
-__device__ __forceinline__ u64 wave_bitonic_sort64(u64 x, int lane) {
-#pragma unroll
-  for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const u64 o = shfl_xor_u64(x, stride, lane);
-      const bool ascending = (lane & size) == 0;
-      const bool lower = (lane & stride) == 0;
-      const u64 mn = x < o ? x : o;
-      const u64 mx = x < o ? o : x;
-      x = (lower == ascending) ? mn : mx;
-    }
-  }
-  return x;
-}
 
 // ------------------------------------------------------------------------------ LDS layout
 
@@ -496,6 +480,105 @@ __device__ void lds_rank_write(const TopkParams& p, int64_t n, int seg, const u6
   }
 }
 
+// The value of lane (lane ^ j) for j in 1..32: a swizzle inside each half-wave for j < 32, a
+// bpermute across the halves for j = 32.
+template <int J>
+__device__ __forceinline__ u32 xor_lane(u32 x, int lane) {
+  if constexpr (J < 32) {
+    return static_cast<u32>(__builtin_amdgcn_ds_swizzle(static_cast<int>(x), (J << 10) | 0x1F));
+  } else {
+    return static_cast<u32>(__builtin_amdgcn_ds_bpermute((lane ^ J) << 2, static_cast<int>(x)));
+  }
+}
+
+// One compare-exchange step of a bitonic network across the wave (one u64 per lane): blocks of
+// K lanes, partners J apart; the lower lane of a pair keeps the smaller value in ascending
+// blocks.
+template <int K, int J>
+__device__ __forceinline__ u64 bitonic_step(u64 x, int lane) {
+  const u32 ylo = xor_lane<J>(static_cast<u32>(x), lane);
+  const u32 yhi = xor_lane<J>(static_cast<u32>(x >> 32), lane);
+  const u64 y = (static_cast<u64>(yhi) << 32) | ylo;
+  const bool keep_min = ((lane & J) == 0) == ((lane & K) == 0);
+  return (y < x) == keep_min ? y : x;
+}
+
+// Ascending bitonic sort of one u64 per lane across a wave64 (21 steps, no LDS storage).
+__device__ __forceinline__ u64 wave_sort64(u64 x, int lane) {
+  x = bitonic_step<2, 1>(x, lane);
+  x = bitonic_step<4, 2>(x, lane);
+  x = bitonic_step<4, 1>(x, lane);
+  x = bitonic_step<8, 4>(x, lane);
+  x = bitonic_step<8, 2>(x, lane);
+  x = bitonic_step<8, 1>(x, lane);
+  x = bitonic_step<16, 8>(x, lane);
+  x = bitonic_step<16, 4>(x, lane);
+  x = bitonic_step<16, 2>(x, lane);
+  x = bitonic_step<16, 1>(x, lane);
+  x = bitonic_step<32, 16>(x, lane);
+  x = bitonic_step<32, 8>(x, lane);
+  x = bitonic_step<32, 4>(x, lane);
+  x = bitonic_step<32, 2>(x, lane);
+  x = bitonic_step<32, 1>(x, lane);
+  x = bitonic_step<64, 32>(x, lane);
+  x = bitonic_step<64, 16>(x, lane);
+  x = bitonic_step<64, 8>(x, lane);
+  x = bitonic_step<64, 4>(x, lane);
+  x = bitonic_step<64, 2>(x, lane);
+  x = bitonic_step<64, 1>(x, lane);
+  return x;
+}
+
+// Ranks the M (<= BLOCK, at most 16 runs of 64) unique entries of `list` (LDS) and writes those
+// of rank < kk to the segment's output row (also to sorted[rank] when sorted is not null).
+// Wave w sorts entries [64w, 64w + 64) in registers (a bitonic network, entries past M padded
+// with ~0, which no candidate equals) and writes the sorted run back in place.  The rank of an
+// entry is then its position in its own run plus, for every other run, the number of that
+// run's entries below it: a 7-step binary search per run, the searches of all runs
+// interleaved.  About M * (runs - 1) * 7 LDS reads in place of the M * M compares of counting
+// against every entry: the long-segment kernel ranks a one-workgroup segment's list of up to
+// 1024 entries with it.  (For the main kernel's lists of 129 to 512 entries its fixed latency
+// of about 1 us, 21 dependent bitonic steps and 7 dependent LDS reads, lost to counting.)
+template <int BLOCK, class E>
+__device__ __forceinline__ void sort_rank_write(const TopkParams& p, int64_t n, int seg, u64* list, int M, int kk,
+                                u64* sorted) {
+  constexpr int NW = BLOCK / 64;
+  static_assert(NW <= 16, "at most 16 runs");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int R = (M + 63) >> 6;  // runs
+  if (wid < R) {
+    const u64 x = tid < M ? list[tid] : ~0ull;
+    list[tid] = wave_sort64(x, lane);
+  }
+  __syncthreads();
+  if (wid < R) {  // every slot of the R runs (the padding holds ~0)
+    const u64 x = list[tid];
+    if (x != ~0ull) {
+      int r = lane;  // entries of its own run below it
+#pragma unroll
+      for (int b = 0; b < NW; ++b) {
+        if (b < R && b != wid) {
+          const u64* run = list + b * 64;
+          int pos = 0;  // entries of run b below x, found MSB first
+#pragma unroll
+          for (int s = 64; s > 0; s >>= 1) {
+            const int q = pos + s;
+            const u64 e = run[(q <= 64 ? q : 64) - 1];
+            pos = (q <= 64 && e < x) ? q : pos;
+          }
+          r += pos;
+        }
+      }
+      if (r < kk) {
+        write_rank<E>(p, n, seg, r, x);
+        if (sorted) sorted[r] = x;
+      }
+    }
+  }
+}
+
 // Ranks the M (<= 16 * S) unique candidates of `list` and writes those of rank < kk (also to
 // sorted[rank] when sorted is not null).  One DPP row (16 lanes) per candidate: lane q of the
 // row compares it with entries q, q + 16, ... (S of them, held in registers, loaded once), and
@@ -554,7 +637,7 @@ __device__ __forceinline__ void sample_segment(const TopkParams& p, const u64* s
 // With top-k sampling on, the ranked entries are also kept in LDS (sm.sel, or sm.area when
 // sm.sel holds the selection) and wave 0 then draws the segment's sample.
 template <int BLOCK, class E>
-__device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int kk, int64_t n,
+__device__ __forceinline__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int kk, int64_t n,
                                  int seg) {
   const int tid = threadIdx.x;
   if (M < kk) kk = M;  // cannot happen (every candidate list holds >= kk entries); keeps it safe
@@ -590,6 +673,9 @@ __device__ void finalize_segment(const TopkParams& p, const Smem& sm, int M, int
     // kk, was measured no faster: tied keys take the select through the index digits).  Longer
     // lists take the select: with 8 waves, ranking 512 entries in full (8 latency-bound LDS
     // passes per wave, two waves per SIMD) ran 66.7 -> 112.3 us on 6000 x 10000, k = 50.
+    // Sorted runs of 64 with binary-search ranks (sort_rank_write) were measured slower here
+    // for lists of 129 to 370 entries (fixed latency of about 1 us: 21 dependent bitonic steps,
+    // then 7 dependent LDS reads): C4 k = 1 8.54 -> 9.36 us, 6000 x 10000 67.0 -> 72.2 us.
     lds_rank_write<BLOCK, E>(p, n, seg, sm.area, M, kk, sm.rank, sampling ? sorted : nullptr);
   } else {
     const u64* sel = sm.area;
@@ -695,8 +781,8 @@ struct GroupWs {
   u64* lists;   // [W][kCandArea]
 };
 
-__device__ __forceinline__ GroupWs group_ws(const TopkParams& p, int seg) {
-  const GroupLayout L = group_layout(p.chunks_per_seg);
+__device__ __forceinline__ GroupWs group_ws(const TopkParams& p, int seg, int members) {
+  const GroupLayout L = group_layout(members);
   unsigned char* b = p.groups + static_cast<size_t>(seg) * L.bytes;
   GroupWs g;
   g.flag = reinterpret_cast<u64*>(b + L.flag);
@@ -1039,7 +1125,7 @@ segmented_topk_kernel(TopkParams p) {
   u64 token = epoch;  // cooperative: this call's token (thread 0 until the broadcast)
   GroupWs g{};
   if constexpr (COOP) {
-    g = group_ws(p, seg);
+    g = group_ws(p, seg, p.chunks_per_seg);
     if (tid == 0) {
       token = call_token(epoch, load_agent(g.gen));
       reinterpret_cast<u64*>(sm.wcnt)[0] = token;
@@ -1733,6 +1819,445 @@ segmented_topk_kernel(TopkParams p) {
   TOPK_TRACE(11);
 }
 
+// ------------------------------------------------------------------------------ long segments
+
+// Loads vectors J0 .. J0 + NV - 1 of chunk cb (positions [lo, hi) valid) as the main kernel
+// loads its chunk: nontemporal 16-byte buffer loads, positions outside [lo, hi) set to the NaN
+// filler.
+template <int BLOCK, int NV, class E>
+__device__ __forceinline__ void load_chunk(const TopkParams& p, int64_t cb, int lo, int hi, int J0, uint4 (&v)[NV]) {
+  constexpr int EV = E::kPerVec;
+  const int tid = threadIdx.x;
+  const unsigned char* cptr = reinterpret_cast<const unsigned char*>(p.base) + cb * E::kBytes;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<unsigned char*>(cptr), static_cast<short>(0), ((hi + EV - 1) & ~(EV - 1)) * E::kBytes,
+      kBufferWord3);
+#pragma unroll
+  for (int jj = 0; jj < NV; ++jj) {
+    const u32x4_t t =
+        __builtin_amdgcn_raw_buffer_load_b128(rsrc, tid * 16, (J0 + jj) * BLOCK * 16, kCachePolicyNT);
+    v[jj] = make_uint4(t.x, t.y, t.z, t.w);
+  }
+#pragma unroll
+  for (int jj = 0; jj < NV; ++jj) {
+    const int j = J0 + jj;
+    if ((j == 0 && lo > 0) || (j + 1) * BLOCK * EV > hi) {
+      const int pos = (j * BLOCK + tid) * EV;
+      if (pos < lo || pos + EV > hi) {
+        u32 w4[4] = {v[jj].x, v[jj].y, v[jj].z, v[jj].w};
+#pragma unroll
+        for (int e = 0; e < EV; ++e) {
+          if (pos + e < lo || pos + e >= hi) E::fill(w4, e);
+        }
+        v[jj] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+      }
+    }
+  }
+}
+
+// Key prefix of the thread's best element over its VPT vectors (a NaN filler only if the thread
+// holds nothing better), as in the main kernel's step 2.
+template <int VPT, class E>
+__device__ __forceinline__ u32 thread_best_key(const uint4 (&v)[VPT], u32 inf) {
+  int m1, m2;
+  if constexpr (E::kBytes == 2) {
+    int mx = vec_gmax(as_s2(vec_max2(v[0])));
+#pragma unroll
+    for (int j = 1; j < VPT; ++j) {
+      const int t = vec_gmax(as_s2(vec_max2(v[j])));
+      mx = mx > t ? mx : t;
+    }
+    m1 = mx;
+    m2 = 32767;
+    if (ballot(m1 < 0)) {
+      short2_t mn = as_s2(vec_min2(v[0]));
+#pragma unroll
+      for (int j = 1; j < VPT; ++j) mn = __builtin_elementwise_min(mn, as_s2(vec_min2(v[j])));
+      m2 = mn.x < mn.y ? mn.x : mn.y;
+    }
+  } else {
+    int mx = vec_max4_i32(v[0]);
+#pragma unroll
+    for (int j = 1; j < VPT; ++j) {
+      const int t = vec_max4_i32(v[j]);
+      mx = mx > t ? mx : t;
+    }
+    m1 = mx;
+    m2 = 0x7fffffff;
+    if (ballot(m1 < 0)) {
+      int mn = vec_min4_i32(v[0]);
+#pragma unroll
+      for (int j = 1; j < VPT; ++j) {
+        const int t = vec_min4_i32(v[j]);
+        mn = mn < t ? mn : t;
+      }
+      m2 = mn;
+    }
+  }
+  const u32 bits = static_cast<u32>(m1 >= 0 ? m1 : m2) & (E::kBytes == 2 ? 0xffffu : 0xffffffffu);
+  return E::prefix(bits, inf);
+}
+
+// Segments longer than one co-resident grid of single-chunk workgroups covers: p.group
+// workgroups per segment (grid seg_num * group), workgroup w taking chunks w, w + group, ...
+// of 1024 threads x 16 vectors.  The steps are those of the cooperative path: the thread bests
+// of every chunk a workgroup takes go into its LDS histograms (high byte, and 32-key bins),
+// which are summed over the segment in one meeting; T is the last key of the fine bin holding
+// the kk-th best; every chunk is read again and its elements with key prefix <= T are listed;
+// the lists meet in one gather and every workgroup ranks a share.  An exact radix refinement
+// over (key, index32) takes over when the lists overflow.  With one workgroup per segment
+// (many segments) nothing is exchanged: the histograms and the list stay in LDS, and the
+// workgroup selects and ranks its segment's list itself.  Every cross-workgroup word carries
+// the per-call token, every wait is bounded, and the segment's status word records a give-up,
+// as on the cooperative path.
+template <class E>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
+long_segment_kernel(TopkParams p) {
+  constexpr int BLOCK = 1024;
+  constexpr int VPT = 16;
+  constexpr int EV = E::kPerVec;
+  constexpr int CH = BLOCK * VPT * EV;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const Smem sm = carve_smem(smem_raw, p.kpad);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int G = p.group;
+  const int seg = static_cast<int>(blockIdx.x) / G;
+  const int w = static_cast<int>(blockIdx.x) - seg * G;
+  const int k = p.k;
+  const u32 inf = p.inf_bits;
+
+  int64_t s0, s1;
+  if (p.offsets) {
+    s0 = p.offsets[seg];
+    s1 = p.offsets[seg + 1];
+    if (s1 < s0) s1 = s0;
+  } else {
+    s0 = static_cast<int64_t>(seg) * p.seg_len;
+    s1 = s0 + p.seg_len;
+  }
+  s0 += p.elem0;
+  s1 += p.elem0;
+  const int64_t n = s1 - s0;
+  const int64_t a0 = s0 & ~static_cast<int64_t>(EV - 1);
+  const int64_t Ws64 = n > 0 ? (s1 - a0 + CH - 1) / CH : 0;
+  if (n <= 0 || n > p.max_len || Ws64 > p.chunks_per_seg) {
+    if (w == 0) {
+      for (int r = tid; r < k; r += BLOCK) write_pad<E>(p, static_cast<int64_t>(seg) * k + r);
+      if (tid == 0) store_agent(p.status + seg, kStatusOk);
+    }
+    return;
+  }
+  const int Ws = static_cast<int>(Ws64);
+  const int arrivals = Ws < G ? Ws : G;  // workgroups of the segment that take chunks
+  if (w >= arrivals) return;
+  const bool solo = arrivals == 1;
+  const int kk = n < k ? static_cast<int>(n) : k;
+  // chunk c of the segment: base cb (16-byte aligned), valid positions [lo, hi)
+  auto chunk_range = [&](int c, int64_t& cb, int& lo, int& hi) {
+    cb = a0 + static_cast<int64_t>(c) * CH;
+    const int64_t c0 = s0 > cb ? s0 : cb;
+    const int64_t c1 = s1 < cb + CH ? s1 : cb + CH;
+    lo = static_cast<int>(c0 - cb);
+    hi = static_cast<int>(c1 - cb);
+  };
+  // Calls fn(raw bits, segment index) for every element of every chunk this workgroup takes,
+  // re-read with plain loads (the refinement passes).
+  auto for_each_element = [&](auto&& fn) {
+    for (int c = w; c < Ws; c += arrivals) {
+      int64_t cb;
+      int lo, hi;
+      chunk_range(c, cb, lo, hi);
+      const unsigned char* cptr = reinterpret_cast<const unsigned char*>(p.base) + cb * E::kBytes;
+      const u32 idx_base = static_cast<u32>(cb - s0);
+#pragma unroll 1
+      for (int j = 0; j < VPT; ++j) {
+        const int pos0 = (j * BLOCK + tid) * EV;
+        if (pos0 < hi && pos0 + EV > lo) {
+          const uint4 x = *reinterpret_cast<const uint4*>(cptr + static_cast<u32>(pos0) * E::kBytes);
+          const u32 w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+          for (int e = 0; e < EV; ++e) {
+            const int pos = pos0 + e;
+            if (pos >= lo && pos < hi) fn(E::element(w4, e), idx_base + static_cast<u32>(pos));
+          }
+        }
+      }
+    }
+  };
+
+  // Call token, status reset and (workgroup 0 of a shared segment) the global histograms'
+  // clear, as on the cooperative path.
+  const u64 epoch = p.epoch;
+  u64 token = epoch;
+  const GroupWs g = group_ws(p, seg, G);
+  if (tid == 0) {
+    if (!solo) token = call_token(epoch, load_agent(g.gen));
+    reinterpret_cast<u64*>(sm.wcnt)[0] = token;
+    if (w == 0) store_agent(p.status + seg, kStatusOk);
+  }
+  if (!solo && w == 0) {
+    for (int i = tid; i < kGroupCopies * 256; i += BLOCK) store_agent(g.hist + i, 0u);
+    for (int i = tid; i < kFineCopies * kFineBins; i += BLOCK) store_agent(g.fine + i, 0u);
+    for (int i = tid; i < kRefineDigits * 256; i += BLOCK) store_agent(g.rhist + i, 0u);
+    wait_vector_memory();
+    __syncthreads();
+    if (tid == 0) store_agent(g.flag, ((token & kTagMask) << 20) | 1u);
+  }
+  u32* fine = reinterpret_cast<u32*>(sm.area);  // 32-key bins, in the (unused) candidate area
+  for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
+  for (int i = tid; i < kFineBins; i += BLOCK) fine[i] = 0;
+  __syncthreads();
+  token = reinterpret_cast<const u64*>(sm.wcnt)[0];
+  const u64 tag = token & kTagMask;
+
+  // ---- A. the thread bests of every chunk this workgroup takes, into the LDS histograms
+  for (int c = w; c < Ws; c += arrivals) {
+    int64_t cb;
+    int lo, hi;
+    chunk_range(c, cb, lo, hi);
+    u32 bk = 0xffffffffu;
+#pragma unroll 1
+    for (int J0 = 0; J0 < VPT; J0 += VPT / 2) {  // half a chunk at a time (register pressure)
+      uint4 v[VPT / 2];
+      load_chunk<BLOCK, VPT / 2, E>(p, cb, lo, hi, J0, v);
+      const u32 hk = thread_best_key<VPT / 2, E>(v, inf);
+      bk = hk < bk ? hk : bk;
+    }
+    atomicAdd(&sm.hist[bk >> 8], 1u);
+    atomicAdd(&fine[bk >> 5], 1u);
+  }
+  __syncthreads();
+  if (!solo) {
+    int late = 0;
+    if (tid == 0) {  // the global histograms are cleared
+      const u32 want = (p.force_timeout & kForceFlagWait) ? 2u : 1u;
+      late = 1;
+      for (u32 spin = 0; spin < p.spin_limit; ++spin) {
+        if (tagged_value(load_agent(g.flag), tag) == want) {
+          late = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    if (__syncthreads_or(late)) {
+      give_up_row<BLOCK, E>(p, seg, g.gen);
+      return;
+    }
+    for (int i = tid; i < kFineBins; i += BLOCK) {
+      const u32 c = fine[i];
+      if (c) {
+        __hip_atomic_fetch_add(g.fine + (w % kFineCopies) * kFineBins + i, c, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    const u64 expect = (p.force_timeout & kForceBarrier) ? (token ^ 1u) : token;
+    if (!group_histogram<BLOCK>(sm.hist, g.hist, sm.stage, g.arrive, token, expect, w, arrivals, p.spin_limit)) {
+      give_up_row<BLOCK, E>(p, seg, g.gen);
+      return;
+    }
+    if (w == 0 && tid == 0) __hip_atomic_fetch_add(g.gen, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // T: the last key of the 32-key bin holding the kk-th smallest thread best (at least kk real
+  // elements are at or below it).
+  if (wid == 0) wave_find_bucket(sm.hist, kk, sm.scal + 8, lane);
+  __syncthreads();
+  const u32 b1 = static_cast<u32>(sm.scal[8]);
+  if (tid < 8 * kFineCopies) {  // the 8 fine bins of bucket b1, copy by copy
+    const int q = tid >> 3;
+    sm.stage[tid] = solo ? (q == 0 ? fine[b1 * 8 + (tid & 7)] : 0u)
+                         : load_agent(g.fine + q * kFineBins + b1 * 8 + (tid & 7));
+  }
+  __syncthreads();
+  if (wid == 0) {
+    u32 c = 0;
+    if (lane < 8) {
+#pragma unroll
+      for (int q = 0; q < kFineCopies; ++q) c += sm.stage[q * 8 + lane];
+    }
+    const u32 incl = wave_inclusive_scan(c);
+    const u32 rest = static_cast<u32>(kk - sm.scal[9]);
+    const u64 m = ballot(lane < 8 && incl >= rest);
+    if (lane == static_cast<int>(__builtin_ctzll(m))) sm.scal[12] = lane;
+  }
+  if (tid == 0) sm.scal[4] = 0;
+  __syncthreads();
+  const u32 T = (((b1 << 3) | static_cast<u32>(sm.scal[12])) << 5) | 31u;
+
+  // ---- B. every chunk again: its elements with key prefix <= T, one ballot per element
+  // position, into per-wave LDS regions that one atomic per wave and chunk places in the list.
+  if (T == 0xffffu) {
+    if (tid == 0) sm.scal[4] = kArea + 1;  // no usable threshold: the refinement decides
+  } else {
+    constexpr int RC = kStageWords / 2;
+    u64* region = reinterpret_cast<u64*>(sm.stage + wid * kStageWords);
+    for (int c = w; c < Ws; c += arrivals) {
+      int64_t cb;
+      int lo, hi;
+      chunk_range(c, cb, lo, hi);
+      const u32 idx_base = static_cast<u32>(cb - s0);
+      u32 wcount = 0;  // wave-uniform
+#pragma unroll 1
+      for (int J0 = 0; J0 < VPT; J0 += VPT / 2) {  // half a chunk at a time (register pressure)
+        uint4 v[VPT / 2];
+        load_chunk<BLOCK, VPT / 2, E>(p, cb, lo, hi, J0, v);
+#pragma unroll
+        for (int jj = 0; jj < VPT / 2; ++jj) {
+          const u32 w4[4] = {v[jj].x, v[jj].y, v[jj].z, v[jj].w};
+#pragma unroll
+          for (int e = 0; e < EV; ++e) {
+            const u32 b = E::element(w4, e);  // positions outside [lo, hi) hold the NaN filler
+            const bool h = E::prefix(b, inf) <= T;
+            const u64 m = ballot(h);
+            if (m) {
+              if (h) {
+                const u32 slot = wcount + mbcnt(m);
+                if (slot < static_cast<u32>(RC))
+                  region[slot] = E::pack(b, idx_base + static_cast<u32>(((J0 + jj) * BLOCK + tid) * EV + e), inf);
+              }
+              wcount += static_cast<u32>(__popcll(m));
+            }
+          }
+        }
+      }
+      const u32 amount = wcount > static_cast<u32>(RC) ? static_cast<u32>(kArea) + 1u : wcount;
+      if (amount) {
+        wave_lds_sync();
+        u32 base = 0;
+        if (lane == 0) base = atomicAdd(reinterpret_cast<u32*>(&sm.scal[4]), amount);
+        base = __builtin_amdgcn_readfirstlane(base);
+        if (wcount <= static_cast<u32>(RC)) {
+          for (u32 i = lane; i < wcount; i += 64) {
+            if (base + i < static_cast<u32>(kArea)) sm.area[base + i] = region[i];
+          }
+        }
+        wave_lds_sync();  // the region is reused by the next chunk
+      }
+    }
+  }
+  __syncthreads();
+  const int C = sm.scal[4];
+
+  // ---- C. the segment's list: every workgroup's list gathered (or the solo list in place);
+  // the refinement when one overflowed or the whole list would not fit the gather.
+  int* cnt = reinterpret_cast<int*>(sm.hist);   // [256] list lengths of the workgroups
+  int* pre = reinterpret_cast<int*>(sm.hist2);  // [256] their exclusive prefix sums
+  u64* mylist = g.lists + static_cast<size_t>(w) * kCandArea;
+  u32 total;
+  if (solo) {
+    total = C > kArea ? kAbsent : static_cast<u32>(C);
+  } else {
+    const u32 contrib = C > kArea ? static_cast<u32>(kCandArea) + 1u : static_cast<u32>(C);
+    if (contrib <= static_cast<u32>(kCandArea)) {
+      for (u32 i = tid; i < contrib; i += BLOCK) store_agent(mylist + i, sm.area[i]);
+    }
+    wait_vector_memory();  // the list is complete before its length announces it
+    __syncthreads();
+    if (tid == 0) store_agent(g.counts + w, (tag << 20) | contrib);
+    const u64 want = (p.force_timeout & kForceCollect) ? (tag ^ 1u) : tag;
+    total = group_collect<BLOCK>(g.counts, g.lists, want, arrivals, sm.area, cnt, pre, sm.scal + 20, p.spin_limit);
+    if (total == kGaveUp) {
+      give_up_row<BLOCK, E>(p, seg, g.gen);
+      return;
+    }
+  }
+  if (total == kAbsent) {
+    // Exact radix refinement of Q = key << 32 | index32 among the elements with key prefix
+    // <= T (one histogram per 8-bit digit, summed over the segment), until at most kCandArea
+    // elements are at or below the bound.
+    u64 prefix = 0, pmask = 0;
+    int rneed = kk;
+    int pass = 0;
+    constexpr u64 kQMask = E::kKeyBits == 32 ? ~0ull : ((1ull << (32 + E::kKeyBits)) - 1);
+    for (int shift = E::kKeyBits + 24; shift >= 0; shift -= 8, ++pass) {
+      for (int i = tid; i < 256; i += BLOCK) sm.hist[i] = 0;
+      __syncthreads();
+      for_each_element([&](u32 b, u32 idx) {
+        const u64 Q = (static_cast<u64>(E::key(b, inf)) << 32) | idx;
+        if (E::prefix(b, inf) <= T && (Q & pmask) == prefix) atomicAdd(&sm.hist[(Q >> shift) & 255u], 1u);
+      });
+      __syncthreads();
+      if (!solo && !group_histogram_single<BLOCK>(sm.hist, g.rhist + pass * 256, g.arrive + (3 + pass) * G, token,
+                                                  w, arrivals, p.spin_limit)) {
+        give_up_row<BLOCK, E>(p, seg, g.gen);
+        return;
+      }
+      if (wid == 0) wave_find_bucket(sm.hist, rneed, sm.scal, lane);
+      __syncthreads();
+      const int b = sm.scal[0];
+      const int before = sm.scal[1];
+      const int cnt_b = sm.scal[2];
+      __syncthreads();
+      rneed -= before;
+      prefix |= static_cast<u64>(b) << shift;
+      pmask |= 0xffull << shift;
+      if ((kk - rneed) + cnt_b <= kCandArea) break;
+    }
+    const u64 bound = prefix | (~pmask & kQMask);
+    if (tid == 0) sm.scal[4] = 0;
+    __syncthreads();
+    for_each_element([&](u32 b, u32 idx) {
+      const u64 Q = (static_cast<u64>(E::key(b, inf)) << 32) | idx;
+      if (E::prefix(b, inf) <= T && Q <= bound) {
+        const int slot = atomicAdd(&sm.scal[4], 1);
+        if (slot < kArea) sm.area[slot] = E::pack(b, idx, inf);
+      }
+    });
+    __syncthreads();
+    const u32 c2 = static_cast<u32>(sm.scal[4] < kArea ? sm.scal[4] : kArea);
+    if (solo) {
+      total = c2;
+    } else {
+      for (u32 i = tid; i < c2; i += BLOCK) store_agent(mylist + i, sm.area[i]);
+      wait_vector_memory();
+      __syncthreads();
+      if (tid == 0) store_agent(g.counts + G + w, (tag << 20) | c2);
+      total = group_collect<BLOCK>(g.counts + G, g.lists, tag, arrivals, sm.area, cnt, pre, sm.scal + 20,
+                                   p.spin_limit);
+      if (total == kGaveUp) {
+        give_up_row<BLOCK, E>(p, seg, g.gen);
+        return;
+      }
+      if (total == kAbsent) total = 0;  // cannot happen: at most kCandArea elements are <= bound
+    }
+  }
+
+  // ---- D. ranks and the output row.  Shared segments rank a share of the list per workgroup
+  // (workgroup 0 also writes the pads); a solo workgroup selects the kk best (radix select)
+  // when the list is longer than a workgroup's threads and ranks them in sorted runs.
+  if (w == 0) {
+    for (int r = kk + tid; r < k; r += BLOCK) write_pad<E>(p, static_cast<int64_t>(seg) * k + r);
+  }
+  const int M = static_cast<int>(total);
+  if (!solo) {
+    const int per = (M + arrivals - 1) / arrivals;
+    const int r0 = w * per < M ? w * per : M;
+    const int r1 = r0 + per < M ? r0 + per : M;
+    rank_range_write<BLOCK, E>(p, n, seg, sm.area, M, kk, r0, r1);
+    return;
+  }
+  u64* list = sm.area;
+  int Ml = M;
+  if (M > BLOCK) {
+    const u64 bound = block_select_bound<BLOCK, E>(sm.area, M, kk, sm.hist, sm.scal, n);
+    if (tid == 0) sm.scal[3] = 0;
+    __syncthreads();
+    for (int i = tid; i < M; i += BLOCK) {
+      const u64 P = sm.area[i];
+      if (P <= bound) {
+        const int slot = atomicAdd(&sm.scal[3], 1);
+        if (slot < p.kpad) sm.sel[slot] = P;
+      }
+    }
+    __syncthreads();
+    list = sm.sel;
+    Ml = kk;
+  }
+  sort_rank_write<BLOCK, E>(p, n, seg, list, Ml, kk, nullptr);
+}
+
 template <int BLOCK, int VPT, class E>
 int launch_shape(const Plan& plan, const TopkParams& params, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(params.seg_num) * params.chunks_per_seg));
@@ -1798,11 +2323,27 @@ int launch_cooperative(const Plan& plan, TopkParams params, hipStream_t stream) 
   return static_cast<int>(hipGetLastError());
 }
 
+// Launch of the long-segment path: seg_num * group workgroups of 1024 threads.  With several
+// workgroups per segment they wait for each other, so (as on the cooperative path) the grid
+// must fit the CUs; one workgroup per segment waits for nothing.
+template <class E>
+int launch_long(const Plan& plan, const TopkParams& params, hipStream_t stream) {
+  const int64_t groups = static_cast<int64_t>(params.seg_num) * params.group;
+  if (params.group > 1 && groups > device_cu_count()) return static_cast<int>(hipErrorCooperativeLaunchTooLarge);
+  hipLaunchKernelGGL((long_segment_kernel<E>), dim3(static_cast<unsigned>(groups)), dim3(1024),
+                     static_cast<unsigned>(plan.lds_bytes), stream, params);
+  return static_cast<int>(hipGetLastError());
+}
+
 // The instantiation for the plan's workgroup shape and element format.
 template <class E>
 int launch_format(const Plan& plan, const TopkParams& params, hipStream_t s) {
   const int b = plan.shape.block;
   const int vpt = plan.shape.vpt;
+  if (plan.group > 0) {
+    if (b != 1024 || vpt != 16) return static_cast<int>(hipErrorInvalidValue);
+    return launch_long<E>(plan, params, s);
+  }
   if (plan.cooperative) {
     if (b != 1024 || vpt != 16) return static_cast<int>(hipErrorInvalidValue);
     return launch_cooperative<E>(plan, params, s);

@@ -80,6 +80,13 @@ def test_workspace_size_contract():
     assert bt.batch_topk_half_workspace_size(1, 10000, 129) > 1
     assert bt.batch_topk_half_workspace_size(128, 128256, 50) > 1
     assert bt.batch_topk_half_workspace_size(256, 32000, 256) > 1
+    # segments up to 2^31 - 1 elements at every k (the long-segment path beyond one
+    # co-resident grid of single-chunk workgroups)
+    for shape in ((1, 50_000_000, 1), (1, 50_000_000, 1024), (4, 20_000_000, 64), (300, 200_000, 1024),
+                  (1, 2**31 - 1, 1024), (2, 2**30, 1), (5000, 400_000, 700)):
+        assert bt.batch_topk_half_workspace_size(*shape) > 1, shape
+    assert bt.batch_topk_half_segmented_workspace_size(218, 131072, 1024) > 1
+    assert bt.batch_topk_half_segmented_workspace_size(3, 2**31 - 1, 64) > 1
     # > 1 so that "workspace_bytes - 1" is a meaningful short workspace (test:1311-1314)
     ws = bt.batch_topk_half_workspace_size(1, 10000, 50)
     assert ws > 1
@@ -147,6 +154,10 @@ def test_kernel_resources_keep_occupancy_without_spills():
     # threshold, each for 16-bit and for 32-bit elements
     assert len(kernels) == 50, sorted(kernels)
     assert sum("Elem32" in k for k in kernels) == 25, sorted(kernels)
+    # and the long-segment kernel for 16-bit and 32-bit elements
+    long_kernels = {k: v for k, v in usage.items() if "long_segment_kernel" in k}
+    assert len(long_kernels) == 2, sorted(long_kernels)
+    kernels.update(long_kernels)
     for name, r in kernels.items():
         assert r["ScratchSize [bytes/lane]"] == 0, (name, r)
         assert r["Occupancy [waves/SIMD]"] >= 4, (name, r)
@@ -179,12 +190,12 @@ def test_f32_entry_points_validate_and_size():
         bt.batch_topk_f32_workspace_size(128, 128256, 50)
     assert bt.batch_topk_ex_workspace_size(bt.FORMAT_F32, True, 4, 1000, 64) == \
         bt.batch_topk_f32_segmented_workspace_size(4, 1000, 64)
-    # a cooperative grid beyond 256 workgroups is unsupported: 2^24 floats with k = 1024 take
-    # 256 chunks when 16-byte aligned (a misaligned pointer is refused at launch); two such
-    # rows take 512
+    # 2^24 floats with k = 1024 take 256 cooperative chunks when 16-byte aligned (a misaligned
+    # pointer is refused at launch); longer rows, or more of them, take the long-segment path
     assert bt.batch_topk_f32_workspace_size(1, 1 << 24, 1024) > 1
-    assert bt.batch_topk_f32_workspace_size(2, 1 << 24, 1024) == 0
-    assert bt.batch_topk_f32_workspace_size(1, (1 << 24) + 1, 1024) == 0
+    assert bt.batch_topk_f32_workspace_size(2, 1 << 24, 1024) > 1
+    assert bt.batch_topk_f32_workspace_size(1, (1 << 24) + 1, 1024) > 1
+    assert bt.batch_topk_f32_workspace_size(1, 2**31 - 1, 1024) > 1
     ws = bt.batch_topk_f32_workspace_size(1, 10000, 50)
     call = bt.batch_topk_f32
     assert call(0, 1, 10000, 50, P_VAL, P_IDX, P_WS, ws) == INVALID
