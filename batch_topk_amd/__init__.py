@@ -48,7 +48,12 @@ EXPORTED_SYMBOLS = (
     "radix_topk_batch_topk_f32_segmented_workspace_size",
     "radix_topk_workspace_status",
     "radix_topk_debug_wait_hook",
+    "radix_topk_batch_topk_half_noalloc",
 )
+
+# radix_topk_batch_topk_half_noalloc: its static per-GPU workspace (include/batch_topk.h)
+NOALLOC_SCRATCH_BYTES = 8 << 20
+HIP_ERROR_OUT_OF_MEMORY = 2
 
 # radix_topk_workspace_status codes (include/batch_topk.h)
 STATUS_OK = 0
@@ -119,6 +124,8 @@ def load_library():
         L.radix_topk_batch_topk_ex_workspace_size.argtypes = [i32, i32, i32, i32, i32]
         L.radix_topk_workspace_status.restype = i32
         L.radix_topk_workspace_status.argtypes = [vp, sz, i32, vp, vp]
+        L.radix_topk_batch_topk_half_noalloc.restype = i32
+        L.radix_topk_batch_topk_half_noalloc.argtypes = [vp, i32, i32, i32, vp, vp, vp]
         L.radix_topk_debug_wait_hook.restype = None
         L.radix_topk_debug_wait_hook.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
         _lib = L
@@ -134,6 +141,14 @@ def batch_topk_half(d_input: int, seg_num: int, seg_len: int, k: int, d_output_v
     return int(load_library().radix_topk_batch_topk_half(
         d_input, seg_num, seg_len, k, d_output_values, d_output_indices, d_workspace,
         workspace_bytes, stream))
+
+
+def batch_topk_half_noalloc(d_input: int, seg_num: int, seg_len: int, k: int, d_output_values: int,
+                            d_output_indices: int, stream: int = 0) -> int:
+    """radix_topk_batch_topk_half_noalloc: batch_topk_half with the library's static per-GPU
+    workspace (no workspace argument, nothing allocated) -> hipError_t code."""
+    return int(load_library().radix_topk_batch_topk_half_noalloc(
+        d_input, seg_num, seg_len, k, d_output_values, d_output_indices, stream))
 
 
 def batch_topk_half_workspace_size(seg_num: int, seg_len: int, k: int) -> int:

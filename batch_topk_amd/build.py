@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libbatch_topk_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-SOURCES = ["topk_kernels.hip", "sample_kernels.hip", "api.cpp"]
+SOURCES = ["topk_kernels.hip", "sample_kernels.hip", "noalloc.hip", "api.cpp"]
 # Measurement reference (not part of the engine): the single-pass read floor, loaded by
 # batch_topk_amd/profiling.py only.
 FLOOR_LIB_PATH = os.path.join(HERE, "libread_floor.so")

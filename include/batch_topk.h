@@ -190,6 +190,25 @@ int radix_topk_batch_topk_ex(const void* d_input, int format, const int32_t* d_o
 size_t radix_topk_batch_topk_ex_workspace_size(int format, int segmented, int seg_num, int seg_len,
                                                int k);
 
+/*
+ * Allocation-free twin of radix_topk_batch_topk_half, for callers that cannot allocate device
+ * memory or pass a workspace (code under HIP-graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The same arguments without the workspace, the same results and the same
+ * rejections (1 = hipErrorInvalidValue before any HIP call); the workspace is instead a static
+ * device array of RADIX_TOPK_NOALLOC_SCRATCH_BYTES bytes, one per GPU, held until the process
+ * ends.  A shape whose workspace (radix_topk_batch_topk_half_workspace_size) exceeds it returns
+ * 2 (hipErrorOutOfMemory) before any HIP call.  Nothing is allocated: the first call on a
+ * device looks up the array's address (hipGetSymbolAddress) and keeps it.  Every call on one
+ * GPU uses the same array, so calls that can overlap on one GPU (different streams, other
+ * host threads) race and must not be issued concurrently; calls in one stream are ordered.
+ * No counterpart in the reference, whose callers always pass a workspace
+ * (reference include/batch_topk.cuh:10-19).
+ */
+#define RADIX_TOPK_NOALLOC_SCRATCH_BYTES (8u << 20)
+int radix_topk_batch_topk_half_noalloc(const uint16_t* d_input, int seg_num, int seg_len, int k,
+                                       uint16_t* d_output_values, int32_t* d_output_indices,
+                                       void* stream);
+
 /* Per-segment completion status of a call (radix_topk_workspace_status). */
 #define RADIX_TOPK_STATUS_OK 0
 #define RADIX_TOPK_STATUS_WAIT_TIMEOUT 1

@@ -101,6 +101,25 @@ def test_workspace_size_contract():
     assert bt.batch_topk_half_segmented_workspace_size(4, 100, 0) == 0
 
 
+def test_noalloc_entry_point_rejects_before_any_hip_call():
+    # invalid arguments as the plain entry point (1), and a shape whose workspace exceeds the
+    # static per-GPU array (2 = hipErrorOutOfMemory), all before any HIP call
+    call = bt.batch_topk_half_noalloc
+    assert call(0, 1, 10000, 50, P_VAL, P_IDX) == INVALID
+    assert call(P_IN, 1, 10000, 50, 0, P_IDX) == INVALID
+    assert call(P_IN, 1, 10000, 50, P_VAL, 0) == INVALID
+    assert call(P_IN, 1, 10, 11, P_VAL, P_IDX) == INVALID
+    assert call(P_IN, 0, 10000, 50, P_VAL, P_IDX) == INVALID
+    assert call(P_IN, 1, 10000, bt.MAX_K + 1, P_VAL, P_IDX) == INVALID
+    big = (100, 20_000_000, 64)
+    assert bt.batch_topk_half_workspace_size(*big) > bt.NOALLOC_SCRATCH_BYTES
+    assert call(P_IN, *big, P_VAL, P_IDX) == bt.HIP_ERROR_OUT_OF_MEMORY
+    # the workloads of the benchmark fit it
+    for shape in ((16, 4096, 50), (128, 128256, 50), (256, 32000, 256), (1, 1 << 24, 1024),
+                  (1, 50_000_000, 1024)):
+        assert 0 < bt.batch_topk_half_workspace_size(*shape) <= bt.NOALLOC_SCRATCH_BYTES, shape
+
+
 def test_validation_rejects_before_any_hip_call():
     ws = bt.batch_topk_half_workspace_size(1, 10000, 50)
     call = bt.batch_topk_half
