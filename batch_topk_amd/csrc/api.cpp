@@ -108,6 +108,17 @@ Plan make_plan(int seg_num, int64_t max_len, int k, int ev = 8, bool shared_alig
       const int64_t w_launch = shared_alignment ? (max_len + chunk - 1) / chunk : W;
       if (static_cast<int64_t>(seg_num) * w_launch <= kMaxCoopGroups) {
         cooperative = true;
+        // Half-length chunks (8 vectors per thread) when that grid fits too: twice as many CUs
+        // pull the segment in (a CU keeps about 64 KB of loads in flight, so 256 KB per CU
+        // arrive in four rounds and 128 KB in two).
+        const int chunk8 = 1024 * 8 * ev;
+        const int64_t W8 = (span + chunk8 - 1) / chunk8;
+        const int64_t w_launch8 = shared_alignment ? (max_len + chunk8 - 1) / chunk8 : W8;
+        if (static_cast<int64_t>(seg_num) * w_launch8 <= kMaxCoopGroups) {
+          vpt = 8;
+          chunk = chunk8;
+          W = W8;
+        }
       } else {
         // The long-segment path: `group` workgroups per segment, each taking every group-th
         // chunk of it, as many per segment as the CUs hold at once for few segments, one per

@@ -2258,45 +2258,75 @@ long_segment_kernel(TopkParams p) {
   sort_rank_write<BLOCK, E>(p, n, seg, list, Ml, kk, nullptr);
 }
 
+// Device attributes the launches use, cached per device: CUs, LDS per CU, LDS per workgroup.
+struct DeviceInfo {
+  int cus;
+  int lds_per_cu;
+  int lds_per_block;
+};
+DeviceInfo device_info() {
+  static std::atomic<int> cached[64][3];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return DeviceInfo{0, 0, 0};
+  if (dev < 64 && cached[dev][0].load(std::memory_order_relaxed) > 0) {
+    return DeviceInfo{cached[dev][0].load(std::memory_order_relaxed), cached[dev][1].load(std::memory_order_relaxed),
+                      cached[dev][2].load(std::memory_order_relaxed)};
+  }
+  DeviceInfo d{0, 0, 0};
+  if (hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return DeviceInfo{0, 0, 0};
+  if (hipDeviceGetAttribute(&d.lds_per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+      hipDeviceGetAttribute(&d.lds_per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) {
+    d.lds_per_cu = d.lds_per_block = 0;  // no spreading (spread_lds)
+  }
+  if (dev < 64) {
+    cached[dev][1].store(d.lds_per_cu, std::memory_order_relaxed);
+    cached[dev][2].store(d.lds_per_block, std::memory_order_relaxed);
+    cached[dev][0].store(d.cus, std::memory_order_relaxed);
+  }
+  return d;
+}
+
+int device_cu_count() { return device_info().cus; }
+
+// Dynamic LDS of a launch of 1024-thread workgroups: when the grid fits the CUs, more than half
+// a CU's LDS, so that the dispatcher gives every workgroup a CU of its own.  (A kernel of at
+// most 64 VGPRs fits twice on a CU: two workgroups placed together share one CU's memory
+// pipeline, about 64 KB of loads in flight, while other CUs stay idle.)
+unsigned spread_lds(size_t lds_bytes, int64_t grid) {
+  const DeviceInfo d = device_info();
+  if (d.cus <= 0 || grid > d.cus || d.lds_per_cu <= 0) return static_cast<unsigned>(lds_bytes);
+  const size_t want = static_cast<size_t>(d.lds_per_cu) / 2 + 256;
+  if (want > static_cast<size_t>(d.lds_per_block)) return static_cast<unsigned>(lds_bytes);
+  return static_cast<unsigned>(lds_bytes > want ? lds_bytes : want);
+}
+
 template <int BLOCK, int VPT, class E>
 int launch_shape(const Plan& plan, const TopkParams& params, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(params.seg_num) * params.chunks_per_seg));
+  const int64_t groups = static_cast<int64_t>(params.seg_num) * params.chunks_per_seg;
+  const dim3 grid(static_cast<unsigned>(groups));
+  const unsigned lds = BLOCK == 1024 ? spread_lds(plan.lds_bytes, groups) : static_cast<unsigned>(plan.lds_bytes);
   // Chunks that can be short (all positions in each thread's first vector, at most 4 * EV * k
   // elements): segmented input, or fixed-length rows that short.
   const int64_t ev = E::kPerVec;
   const bool short_chunks = params.offsets != nullptr ||
                             (params.seg_len + ev - 1 <= BLOCK * ev && params.seg_len <= 4 * ev * params.k);
   if (short_chunks) {
-    hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT, false, E, true>), grid, dim3(BLOCK),
-                       static_cast<unsigned>(plan.lds_bytes), stream, params);
+    hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT, false, E, true>), grid, dim3(BLOCK), lds, stream,
+                       params);
     return static_cast<int>(hipGetLastError());
   }
-  hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT, false, E>), grid, dim3(BLOCK),
-                     static_cast<unsigned>(plan.lds_bytes), stream, params);
+  hipLaunchKernelGGL((segmented_topk_kernel<BLOCK, VPT, false, E>), grid, dim3(BLOCK), lds, stream, params);
   return static_cast<int>(hipGetLastError());
 }
 
-// Launch of the cooperative path.  Its workgroups wait for each other, so all of them must be
-// resident at once: one 1024-thread workgroup fits every CU, and the grid is refused
-// (hipErrorCooperativeLaunchTooLarge) when it has more workgroups than the device has CUs.
+// Launch of the cooperative path (1024 threads, 16 or 8 vectors each).  Its workgroups wait
+// for each other, so all of them must be resident at once: one 1024-thread workgroup fits every
+// CU, and the grid is refused (hipErrorCooperativeLaunchTooLarge) when it has more workgroups
+// than the device has CUs.
 // Within that bound an ordinary launch places every workgroup immediately (kernels of other
 // streams only delay the placement; they do not wait for this one), and it costs far less
 // than hipLaunchCooperativeKernel.  BATCH_TOPK_AMD_COOPERATIVE_LAUNCH=1 selects the runtime's
 // cooperative launch, which checks co-residency itself.
-int device_cu_count() {
-  static std::atomic<int> cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  if (dev < 64) {
-    const int c = cached[dev].load(std::memory_order_relaxed);
-    if (c > 0) return c;
-  }
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
-  return cus;
-}
-
 bool formal_cooperative_launch() {
   static const bool on = [] {
     const char* e = std::getenv("BATCH_TOPK_AMD_COOPERATIVE_LAUNCH");
@@ -2305,20 +2335,20 @@ bool formal_cooperative_launch() {
   return on;
 }
 
-template <class E>
+template <int VPT, class E>
 int launch_cooperative(const Plan& plan, TopkParams params, hipStream_t stream) {
   const int64_t groups = static_cast<int64_t>(params.seg_num) * params.chunks_per_seg;
   if (groups > device_cu_count()) return static_cast<int>(hipErrorCooperativeLaunchTooLarge);
   const dim3 grid(static_cast<unsigned>(groups));
+  const unsigned lds = spread_lds(plan.lds_bytes, groups);
   if (formal_cooperative_launch()) {
     void* args[] = {&params};
     const hipError_t e = hipLaunchCooperativeKernel(
-        reinterpret_cast<const void*>(&segmented_topk_kernel<1024, 16, true, E>), grid, dim3(1024), args,
-        static_cast<unsigned>(plan.lds_bytes), stream);
+        reinterpret_cast<const void*>(&segmented_topk_kernel<1024, VPT, true, E>), grid, dim3(1024), args, lds,
+        stream);
     if (e != hipSuccess) return static_cast<int>(e);
   } else {
-    hipLaunchKernelGGL((segmented_topk_kernel<1024, 16, true, E>), grid, dim3(1024),
-                       static_cast<unsigned>(plan.lds_bytes), stream, params);
+    hipLaunchKernelGGL((segmented_topk_kernel<1024, VPT, true, E>), grid, dim3(1024), lds, stream, params);
   }
   return static_cast<int>(hipGetLastError());
 }
@@ -2331,7 +2361,7 @@ int launch_long(const Plan& plan, const TopkParams& params, hipStream_t stream) 
   const int64_t groups = static_cast<int64_t>(params.seg_num) * params.group;
   if (params.group > 1 && groups > device_cu_count()) return static_cast<int>(hipErrorCooperativeLaunchTooLarge);
   hipLaunchKernelGGL((long_segment_kernel<E>), dim3(static_cast<unsigned>(groups)), dim3(1024),
-                     static_cast<unsigned>(plan.lds_bytes), stream, params);
+                     spread_lds(plan.lds_bytes, groups), stream, params);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -2345,8 +2375,9 @@ int launch_format(const Plan& plan, const TopkParams& params, hipStream_t s) {
     return launch_long<E>(plan, params, s);
   }
   if (plan.cooperative) {
-    if (b != 1024 || vpt != 16) return static_cast<int>(hipErrorInvalidValue);
-    return launch_cooperative<E>(plan, params, s);
+    if (b == 1024 && vpt == 16) return launch_cooperative<16, E>(plan, params, s);
+    if (b == 1024 && vpt == 8) return launch_cooperative<8, E>(plan, params, s);
+    return static_cast<int>(hipErrorInvalidValue);
   }
   if (b == 256 && vpt == 2) return launch_shape<256, 2, E>(plan, params, s);
   if (b == 256 && vpt == 4) return launch_shape<256, 4, E>(plan, params, s);

@@ -169,10 +169,10 @@ def test_kernel_resources_keep_occupancy_without_spills():
 
     usage = resource_usage()
     kernels = {k: v for k, v in usage.items() if "segmented_topk_kernel" in k}
-    # 12 workgroup shapes + the cooperative one, plus the 12 shapes again with the short-chunk
-    # threshold, each for 16-bit and for 32-bit elements
-    assert len(kernels) == 50, sorted(kernels)
-    assert sum("Elem32" in k for k in kernels) == 25, sorted(kernels)
+    # 12 workgroup shapes + the two cooperative ones (8 and 16 vectors), plus the 12 shapes again
+    # with the short-chunk threshold, each for 16-bit and for 32-bit elements
+    assert len(kernels) == 52, sorted(kernels)
+    assert sum("Elem32" in k for k in kernels) == 26, sorted(kernels)
     # and the long-segment kernel for 16-bit and 32-bit elements
     long_kernels = {k: v for k, v in usage.items() if "long_segment_kernel" in k}
     assert len(long_kernels) == 2, sorted(long_kernels)
