@@ -222,6 +222,31 @@ __device__ __forceinline__ u32 wave_or(u32 x) {
   return static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(x), 63));
 }
 
+// One step of a wave minimum over u64 with DPP: lanes without a source lane (and rows the row
+// mask leaves out) see ~0, the identity of the minimum.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ u64 dpp_min_u64(u64 x) {
+  const u32 lo = static_cast<u32>(__builtin_amdgcn_update_dpp(-1, static_cast<int>(static_cast<u32>(x)), CTRL,
+                                                               ROW_MASK, 0xf, false));
+  const u32 hi = static_cast<u32>(__builtin_amdgcn_update_dpp(-1, static_cast<int>(static_cast<u32>(x >> 32)), CTRL,
+                                                               ROW_MASK, 0xf, false));
+  const u64 y = (static_cast<u64>(hi) << 32) | lo;
+  return y < x ? y : x;
+}
+
+// Minimum of x over the wave (DPP min-scan; lane 63 holds it), returned wave-uniform.
+__device__ __forceinline__ u64 wave_min_u64(u64 x) {
+  x = dpp_min_u64<0x111, 0xf>(x);
+  x = dpp_min_u64<0x112, 0xf>(x);
+  x = dpp_min_u64<0x114, 0xf>(x);
+  x = dpp_min_u64<0x118, 0xf>(x);
+  x = dpp_min_u64<0x142, 0xa>(x);
+  x = dpp_min_u64<0x143, 0xc>(x);
+  const u32 lo = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(x)), 63));
+  const u32 hi = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(x >> 32)), 63));
+  return (static_cast<u64>(hi) << 32) | lo;
+}
+
 // Inclusive prefix sum across a wave64 with DPP: row_shr 1/2/4/8 inside each 16-lane row,
 // then row_bcast:15 and row_bcast:31 carry the row totals upward.
 __device__ __forceinline__ u32 wave_inclusive_scan(u32 x) {
@@ -1241,6 +1266,58 @@ segmented_topk_kernel(TopkParams p) {
   const u32 best_key = E::prefix(best_bits, inf);
   TOPK_TRACE(1);
   TOPK_WTRACE(1);
+
+  // ---- k = 1 (16-bit single-chunk rows, no sampling): the chunk's best element directly.  T
+  // is the smallest thread best key, a workgroup minimum (a thread best is a real element, so
+  // the best element has key <= T).  For a positive T, the elements at or below it are found
+  // as step 4 finds them (a vector can hold one only if its int16 max reaches raw(T), then an
+  // exact test per element), and the smallest (key, position) of them is a second workgroup
+  // minimum.  No list and no ranking.  A non-positive T (rows of no positive value) takes
+  // the general path.
+  if constexpr (!COOP && E::kBytes == 2) {
+    if (k == 1 && Ws == 1 && !p.samples) {  // workgroup-uniform
+      u64* wmin = sm.area;  // [NW] per-wave minima
+      const u64 wt = wave_min_u64(best_key);
+      if (lane == 0) wmin[wid] = wt;
+      __syncthreads();
+      u32 Ta = 0xffffffffu;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) Ta = static_cast<u32>(wmin[q]) < Ta ? static_cast<u32>(wmin[q]) : Ta;
+      if (Ta < 0x7fffu) {  // workgroup-uniform
+        const u32 t_lo = Ta ^ 0x7fffu;  // raw bits of T: candidates are b in [t_lo, inf]
+        const u32 span = inf - t_lo;
+        u64 mine = ~0ull;  // this thread's smallest (key << 32 | position) at or below T
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+          if (gv[j] >= static_cast<int>(t_lo)) {
+            const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+            for (int e = 0; e < EV; ++e) {
+              const u32 b = E::element(w4, e);
+              if (b - t_lo <= span) {  // t_lo <= b <= inf, as unsigned
+                const u64 P = (static_cast<u64>(b ^ 0x7fffu) << 32) | static_cast<u32>((j * BLOCK + tid) * EV + e);
+                mine = P < mine ? P : mine;
+              }
+            }
+          }
+        }
+        const u64 wbest = wave_min_u64(mine);
+        __syncthreads();  // every wave has read the thread-best minima
+        if (lane == 0) wmin[wid] = wbest;
+        __syncthreads();
+        if (tid == 0) {
+          u64 P = wmin[0];
+#pragma unroll
+          for (int q = 1; q < NW; ++q) P = wmin[q] < P ? wmin[q] : P;
+          const u32 raw = static_cast<u32>(P >> 32) ^ 0x7fffu;
+          p.out_idx[seg] = static_cast<int>(idx_base + static_cast<u32>(P));
+          if (p.out_vals) static_cast<uint16_t*>(p.out_vals)[seg] = static_cast<uint16_t>(raw);
+        }
+        return;
+      }
+      __syncthreads();  // the general path reuses the candidate area
+    }
+  }
 
   // ---- 3. threshold T.  A single workgroup: the kc-th smallest thread best, exactly, by two
   // LDS histogram passes (high byte, then low byte inside the boundary bucket).  A cooperative
