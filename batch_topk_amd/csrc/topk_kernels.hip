@@ -121,6 +121,7 @@ constexpr int kBufferWord3 = 0x00020000;
 constexpr int kCachePolicyNT = 2;
 constexpr int kArea = kCandArea;        // LDS candidate entries (candidate list, merged lists)
 constexpr int kRankCap = 512;           // rank-counting path handles up to this many
+constexpr int kSortRankMin = 256;       // lists at least this long are ranked by sorted runs
 
 // ------------------------------------------------------------------------------ codec
 
@@ -505,68 +506,160 @@ __device__ void lds_rank_write(const TopkParams& p, int64_t n, int seg, const u6
   }
 }
 
-// The value of lane (lane ^ j) for j in 1..32: a swizzle inside each half-wave for j < 32, a
-// bpermute across the halves for j = 32.
-template <int J>
-__device__ __forceinline__ u32 xor_lane(u32 x, int lane) {
-  if constexpr (J < 32) {
-    return static_cast<u32>(__builtin_amdgcn_ds_swizzle(static_cast<int>(x), (J << 10) | 0x1F));
-  } else {
-    return static_cast<u32>(__builtin_amdgcn_ds_bpermute((lane ^ J) << 2, static_cast<int>(x)));
+// lds_rank_write for 16-bit elements in segments of at most 65,536 elements: the count runs
+// on 32-bit words (key16 << 16 | index16, ordered as the packed candidates are, since
+// indices are unique) staged in `keys` (LDS, 16-byte aligned, M + 3 words), so one 16-byte
+// broadcast read brings four entries and each compare is a 32-bit one.
+template <int BLOCK, class E>
+__device__ void lds_rank_write16(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
+                                 int kk, int* rank, u32* keys, u64* sorted) {
+  constexpr int NW = BLOCK / 64;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int G = (M + 127) >> 7;                  // candidate groups of 128 (two per lane)
+  const int Q = G >= NW ? 1 : NW / G;            // waves sharing one group's entry range
+  const int span = ((M + Q - 1) / Q + 15) & ~15;  // entries per share, a multiple of 16
+  for (int i = threadIdx.x; i < M; i += BLOCK) {
+    const u64 P = list[i];
+    keys[i] = (static_cast<u32>(P >> 48) << 16) | (static_cast<u32>(P >> 16) & 0xffffu);
+    rank[i] = 0;
+  }
+  __syncthreads();
+  TOPK_WTRACE(6);
+  const uint4* quads = reinterpret_cast<const uint4*>(keys);
+  for (int u = wid; u < G * Q; u += NW) {
+    const int g = u % G;
+    const int q = u / G;
+    const int i0 = g * 128 + lane;
+    const int i1 = i0 + 64;
+    const u32 x0 = i0 < M ? keys[i0] : 0u;
+    const u32 x1 = i1 < M ? keys[i1] : 0u;
+    const int j0 = q * span;
+    const int j1 = j0 + span < M ? j0 + span : M;
+    u32 c0 = 0, c1 = 0;
+    int j = j0;
+    // 32 entries (eight reads in flight) per step, then steps of 4, then single entries
+    for (; j + 32 <= j1; j += 32) {
+      uint4 a[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = quads[(j >> 2) + e];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        c0 += (a[e].x < x0 ? 1u : 0u) + (a[e].y < x0 ? 1u : 0u) + (a[e].z < x0 ? 1u : 0u) + (a[e].w < x0 ? 1u : 0u);
+        c1 += (a[e].x < x1 ? 1u : 0u) + (a[e].y < x1 ? 1u : 0u) + (a[e].z < x1 ? 1u : 0u) + (a[e].w < x1 ? 1u : 0u);
+      }
+    }
+    for (; j + 4 <= j1; j += 4) {
+      const uint4 a = quads[j >> 2];
+      c0 += (a.x < x0 ? 1u : 0u) + (a.y < x0 ? 1u : 0u) + (a.z < x0 ? 1u : 0u) + (a.w < x0 ? 1u : 0u);
+      c1 += (a.x < x1 ? 1u : 0u) + (a.y < x1 ? 1u : 0u) + (a.z < x1 ? 1u : 0u) + (a.w < x1 ? 1u : 0u);
+    }
+    for (; j < j1; ++j) {
+      const u32 v = keys[j];
+      c0 += v < x0 ? 1u : 0u;
+      c1 += v < x1 ? 1u : 0u;
+    }
+    if (i0 < M && c0) atomicAdd(&rank[i0], static_cast<int>(c0));
+    if (i1 < M && c1) atomicAdd(&rank[i1], static_cast<int>(c1));
+  }
+  TOPK_WTRACE(7);
+  __syncthreads();
+  for (int i = threadIdx.x; i < M; i += BLOCK) {
+    const int r = rank[i];
+    if (r < kk) {
+      const u64 x = list[i];
+      write_rank<E>(p, n, seg, r, x);
+      if (sorted) sorted[r] = x;
+    }
   }
 }
 
-// One compare-exchange step of a bitonic network across the wave (one u64 per lane): blocks of
-// K lanes, partners J apart; the lower lane of a pair keeps the smaller value in ascending
-// blocks.
-template <int K, int J>
-__device__ __forceinline__ u64 bitonic_step(u64 x, int lane) {
-  const u32 ylo = xor_lane<J>(static_cast<u32>(x), lane);
-  const u32 yhi = xor_lane<J>(static_cast<u32>(x >> 32), lane);
-  const u64 y = (static_cast<u64>(yhi) << 32) | ylo;
-  const bool keep_min = ((lane & J) == 0) == ((lane & K) == 0);
-  return (y < x) == keep_min ? y : x;
+// The value of lane (lane ^ M) for the masks a sorting network of 64 lanes uses.  Inside a
+// 16-lane row DPP moves it with no LDS round trip: quad permutations for 1, 2 and 3, the row
+// half-mirror and mirror for 7 and 15, a row rotation for 8 and two rotations and a select
+// for 4 (row_ror:n gives lane i the value of lane (i - n) mod 16).  Across rows a swizzle
+// (16, 31, inside each half-wave) or a bpermute (63).
+template <int CTRL>
+__device__ __forceinline__ u32 dpp_mov(u32 x) {
+  return static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, 0xf, 0xf, false));
+}
+template <int M>
+__device__ __forceinline__ u32 xor_lane(u32 x, int lane) {
+  if constexpr (M == 1) {
+    return dpp_mov<0xB1>(x);  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return dpp_mov<0x4E>(x);  // quad_perm [2,3,0,1]
+  } else if constexpr (M == 3) {
+    return dpp_mov<0x1B>(x);  // quad_perm [3,2,1,0]
+  } else if constexpr (M == 4) {
+    const u32 down = dpp_mov<0x124>(x);  // lane i - 4
+    const u32 up = dpp_mov<0x12C>(x);    // lane i + 4 (i - 12 mod 16)
+    return (lane & 4) ? down : up;
+  } else if constexpr (M == 7) {
+    return dpp_mov<0x141>(x);  // row_half_mirror
+  } else if constexpr (M == 8) {
+    return dpp_mov<0x128>(x);  // row_ror:8
+  } else if constexpr (M == 15) {
+    return dpp_mov<0x140>(x);  // row_mirror
+  } else if constexpr (M == 16 || M == 31) {
+    return static_cast<u32>(__builtin_amdgcn_ds_swizzle(static_cast<int>(x), (M << 10) | 0x1F));
+  } else {
+    static_assert(M == 63, "lane masks of the 64-lane network");
+    return static_cast<u32>(__builtin_amdgcn_ds_bpermute((lane ^ 63) << 2, static_cast<int>(x)));
+  }
 }
 
-// Ascending bitonic sort of one u64 per lane across a wave64 (21 steps, no LDS storage).
+// One compare-exchange step of an ascending sorting network across the wave (one u64 per
+// lane, all values distinct or equal pads): lane i pairs with lane i ^ M, and of each pair the
+// lane whose bit HI is clear keeps the smaller value.
+template <int M, int HI>
+__device__ __forceinline__ u64 sort_step(u64 x, int lane) {
+  const u32 ylo = xor_lane<M>(static_cast<u32>(x), lane);
+  const u32 yhi = xor_lane<M>(static_cast<u32>(x >> 32), lane);
+  const u64 y = (static_cast<u64>(yhi) << 32) | ylo;
+  const bool take = (y < x) != ((lane & HI) != 0);
+  return take ? y : x;
+}
+
+// Ascending bitonic sort of one u64 per lane across a wave64, in the form whose comparators
+// all point one way: merging two sorted runs of K/2 starts with the mirror step (lane i
+// against lane i ^ (K - 1)), then half-cleaners K/4 .. 1.  21 steps; 18 of them stay in DPP.
 __device__ __forceinline__ u64 wave_sort64(u64 x, int lane) {
-  x = bitonic_step<2, 1>(x, lane);
-  x = bitonic_step<4, 2>(x, lane);
-  x = bitonic_step<4, 1>(x, lane);
-  x = bitonic_step<8, 4>(x, lane);
-  x = bitonic_step<8, 2>(x, lane);
-  x = bitonic_step<8, 1>(x, lane);
-  x = bitonic_step<16, 8>(x, lane);
-  x = bitonic_step<16, 4>(x, lane);
-  x = bitonic_step<16, 2>(x, lane);
-  x = bitonic_step<16, 1>(x, lane);
-  x = bitonic_step<32, 16>(x, lane);
-  x = bitonic_step<32, 8>(x, lane);
-  x = bitonic_step<32, 4>(x, lane);
-  x = bitonic_step<32, 2>(x, lane);
-  x = bitonic_step<32, 1>(x, lane);
-  x = bitonic_step<64, 32>(x, lane);
-  x = bitonic_step<64, 16>(x, lane);
-  x = bitonic_step<64, 8>(x, lane);
-  x = bitonic_step<64, 4>(x, lane);
-  x = bitonic_step<64, 2>(x, lane);
-  x = bitonic_step<64, 1>(x, lane);
+  x = sort_step<1, 1>(x, lane);
+  x = sort_step<3, 2>(x, lane);
+  x = sort_step<1, 1>(x, lane);
+  x = sort_step<7, 4>(x, lane);
+  x = sort_step<2, 2>(x, lane);
+  x = sort_step<1, 1>(x, lane);
+  x = sort_step<15, 8>(x, lane);
+  x = sort_step<4, 4>(x, lane);
+  x = sort_step<2, 2>(x, lane);
+  x = sort_step<1, 1>(x, lane);
+  x = sort_step<31, 16>(x, lane);
+  x = sort_step<8, 8>(x, lane);
+  x = sort_step<4, 4>(x, lane);
+  x = sort_step<2, 2>(x, lane);
+  x = sort_step<1, 1>(x, lane);
+  x = sort_step<63, 32>(x, lane);
+  x = sort_step<16, 16>(x, lane);
+  x = sort_step<8, 8>(x, lane);
+  x = sort_step<4, 4>(x, lane);
+  x = sort_step<2, 2>(x, lane);
+  x = sort_step<1, 1>(x, lane);
   return x;
 }
 
 // Ranks the M (<= BLOCK, at most 16 runs of 64) unique entries of `list` (LDS) and writes those
 // of rank < kk to the segment's output row (also to sorted[rank] when sorted is not null).
-// Wave w sorts entries [64w, 64w + 64) in registers (a bitonic network, entries past M padded
-// with ~0, which no candidate equals) and writes the sorted run back in place.  The rank of an
-// entry is then its position in its own run plus, for every other run, the number of that
-// run's entries below it: a 7-step binary search per run, the searches of all runs
-// interleaved.  About M * (runs - 1) * 7 LDS reads in place of the M * M compares of counting
-// against every entry: the long-segment kernel ranks a one-workgroup segment's list of up to
-// 1024 entries with it.  (For the main kernel's lists of 129 to 512 entries its fixed latency
-// of about 1 us, 21 dependent bitonic steps and 7 dependent LDS reads, lost to counting.)
+// Wave w sorts entries [64w, 64w + 64) in registers (wave_sort64; entries past M padded with
+// ~0, which no candidate equals) and writes the sorted run back in place.  The rank of an
+// entry is then the number of entries below it in every run, its own included (where that is
+// its position): a 7-step binary search per run, eight runs' searches interleaved so their
+// LDS reads are in flight together.  About M * runs * 7 LDS reads in place of the M * M
+// compares of counting against every entry.
 template <int BLOCK, class E>
 __device__ __forceinline__ void sort_rank_write(const TopkParams& p, int64_t n, int seg, u64* list, int M, int kk,
-                                u64* sorted) {
+                                                u64* sorted) {
   constexpr int NW = BLOCK / 64;
   static_assert(NW <= 16, "at most 16 runs");
   const int tid = threadIdx.x;
@@ -581,19 +674,25 @@ __device__ __forceinline__ void sort_rank_write(const TopkParams& p, int64_t n, 
   if (wid < R) {  // every slot of the R runs (the padding holds ~0)
     const u64 x = list[tid];
     if (x != ~0ull) {
-      int r = lane;  // entries of its own run below it
+      int r = 0;
+      for (int b0 = 0; b0 < R; b0 += 8) {  // uniform
+        const u64* run[8];
+        int pos[8];
 #pragma unroll
-      for (int b = 0; b < NW; ++b) {
-        if (b < R && b != wid) {
-          const u64* run = list + b * 64;
-          int pos = 0;  // entries of run b below x, found MSB first
+        for (int i = 0; i < 8; ++i) {
+          run[i] = list + 64 * (b0 + i < R ? b0 + i : wid);  // past R: a real run, not counted
+          pos[i] = 0;
+        }
+        // entries of each run below x: pos advances by s while entry pos + s - 1 is below x
 #pragma unroll
-          for (int s = 64; s > 0; s >>= 1) {
-            const int q = pos + s;
-            const u64 e = run[(q <= 64 ? q : 64) - 1];
-            pos = (q <= 64 && e < x) ? q : pos;
-          }
-          r += pos;
+        for (int s = 32; s > 0; s >>= 1) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) pos[i] += run[i][pos[i] + s - 1] < x ? s : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          pos[i] += run[i][pos[i]] < x ? 1 : 0;  // pos <= 63 here; all 64 below gives 64
+          r += b0 + i < R ? pos[i] : 0;
         }
       }
       if (r < kk) {
@@ -698,10 +797,17 @@ __device__ __forceinline__ void finalize_segment(const TopkParams& p, const Smem
     // kk, was measured no faster: tied keys take the select through the index digits).  Longer
     // lists take the select: with 8 waves, ranking 512 entries in full (8 latency-bound LDS
     // passes per wave, two waves per SIMD) ran 66.7 -> 112.3 us on 6000 x 10000, k = 50.
-    // Sorted runs of 64 with binary-search ranks (sort_rank_write) were measured slower here
-    // for lists of 129 to 370 entries (fixed latency of about 1 us: 21 dependent bitonic steps,
-    // then 7 dependent LDS reads): C4 k = 1 8.54 -> 9.36 us, 6000 x 10000 67.0 -> 72.2 us.
-    lds_rank_write<BLOCK, E>(p, n, seg, sm.area, M, kk, sm.rank, sampling ? sorted : nullptr);
+    // Counting costs M * M compares, VALU-bound on the four SIMDs (about 2 us at M = 370);
+    // sorted runs cost a fixed 21 DPP steps and 7 LDS levels.  Measured on 256 x 32000 fp16
+    // rows of 256 distinct values: k = 256 (lists of about 370) 11.2 -> 9.4 us and k = 128
+    // 9.5 -> 9.2 us with runs; with runs from 129 or 160 entries on, k = 64 lost 0.2-0.5 us.
+    if (M >= kSortRankMin) {
+      sort_rank_write<BLOCK, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
+    } else if (E::kBytes == 2 && n <= 0x10000) {
+      lds_rank_write16<BLOCK, E>(p, n, seg, sm.area, M, kk, sm.rank, sm.stage, sampling ? sorted : nullptr);
+    } else {
+      lds_rank_write<BLOCK, E>(p, n, seg, sm.area, M, kk, sm.rank, sampling ? sorted : nullptr);
+    }
   } else {
     const u64* sel = sm.area;
     if (M > kk) {
