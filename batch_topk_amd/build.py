@@ -6,10 +6,12 @@ The library is built in-tree so that it travels with the source tree.
 
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -45,16 +47,28 @@ def hipcc() -> str:
     return path
 
 
-def _compile(sources, out_path: str, verbose: bool, defines=()) -> None:
-    tmp = out_path + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, *[f"-D{d}" for d in defines], "-shared", "-o", tmp,
-           *[os.path.join(CSRC, s) for s in sources], "-lamdhip64"]
+def _run(cmd, verbose: bool, what: str) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed to build " + os.path.basename(out_path))
+        raise RuntimeError("hipcc failed to build " + what)
+
+
+def _object(source: str, out_dir: str, verbose: bool, defines=()) -> str:
+    """One translation unit compiled to an object (host code and its gfx950 device code)."""
+    tag = "_".join(d.lower() for d in defines)
+    obj = os.path.join(out_dir, os.path.splitext(source)[0] + (("." + tag) if tag else "") + ".o")
+    _run([hipcc(), *HIP_FLAGS, *[f"-D{d}" for d in defines], "-c", "-o", obj, os.path.join(CSRC, source)],
+         verbose, source)
+    return obj
+
+
+def _link(objects, out_path: str, verbose: bool) -> None:
+    tmp = out_path + ".tmp"
+    _run([hipcc(), *HIP_FLAGS, "-shared", "-o", tmp, *objects, "-lamdhip64"], verbose,
+         os.path.basename(out_path))
     os.replace(tmp, out_path)
 
 
@@ -75,10 +89,20 @@ def build_cpp_caller(verbose: bool = False) -> str:
 
 def build(verbose: bool = False) -> str:
     """Always recompiles (the build check must exercise the compiler): the engine library, the
-    two measurement libraries (read floor, phase-traced engine) and the drop-in C++ caller."""
-    _compile(SOURCES, LIB_PATH, verbose)
-    _compile(FLOOR_SOURCES, FLOOR_LIB_PATH, verbose)
-    _compile(SOURCES, TRACE_LIB_PATH, verbose, defines=("TOPK_PHASE_TRACE",))
+    two measurement libraries (read floor, phase-traced engine) and the drop-in C++ caller.
+    The translation units compile in parallel into a temporary directory, then link."""
+    jobs = [(src, ()) for src in SOURCES] + [("topk_kernels.hip", ("TOPK_PHASE_TRACE",))]
+    jobs += [(src, ()) for src in FLOOR_SOURCES]
+    with tempfile.TemporaryDirectory(prefix="batch_topk_amd_build_") as out_dir:
+        with concurrent.futures.ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1)) as pool:
+            futures = [pool.submit(_object, src, out_dir, verbose, defs) for src, defs in jobs]
+            objs = [f.result() for f in futures]
+        engine = objs[:len(SOURCES)]
+        trace = [objs[len(SOURCES)] if src == "topk_kernels.hip" else o for src, o in zip(SOURCES, engine)]
+        floor = objs[len(SOURCES) + 1:]
+        _link(engine, LIB_PATH, verbose)
+        _link(trace, TRACE_LIB_PATH, verbose)
+        _link(floor, FLOOR_LIB_PATH, verbose)
     build_cpp_caller(verbose)
     return LIB_PATH
 

@@ -26,11 +26,13 @@
       fp32 on every workload; the unsorted and indices-only outputs), as a markdown table.
 
   python -m batch_topk_amd.profiling phases [--workload W | --shape SEGxLEN] [--k K] [--b2b N]
+        [--per-wave]
       Step timeline of the top-k kernel on an fp16 workload, from the phase-traced build of
       the engine (libbatch_topk_amd_trace.so): per-workgroup stamps of the last of N
       back-to-back calls, on the GPU's constant 100 MHz clock from the first workgroup's
-      start, and per-wave stamps on the shader clock from the wave's workgroup start.  The
-      stamps cost time themselves (the traced build runs about 1 us slower per call).
+      start, and per-wave stamps on the shader clock from the wave's workgroup start (with
+      --per-wave also the median of each wave step by wave index).  The stamps cost time
+      themselves (the traced build runs about 1 us slower per call).
 """
 
 from __future__ import annotations
@@ -42,6 +44,7 @@ import glob
 import json
 import os
 import sys
+import warnings
 
 KERNEL_SUBSTRING = "segmented_topk_kernel"
 COPY_SUBSTRING = "CUDAFunctorOnSelf_add"
@@ -167,7 +170,7 @@ WAVE_PHASES = ((1, "thread best"), (0, "threshold read"), (2, "filter start"), (
                (4, "flushed"), (5, "after filter barrier"), (6, "ranking start"), (7, "ranking end"))
 
 
-def run_phases(workload: str, k: int, b2b: int, shape: str | None = None) -> None:
+def run_phases(workload: str, k: int, b2b: int, shape: str | None = None, per_wave: bool = False) -> None:
     import ctypes
 
     import numpy as np
@@ -271,6 +274,16 @@ def run_phases(workload: str, k: int, b2b: int, shape: str | None = None) -> Non
             m = W[:, :, j] > 0
             if m.any():
                 row(name, ((W[:, :, j] - C[:, 0:1]) / ticks_per_ns)[m])
+        if per_wave:
+            print("wave step by wave index (median ns from its workgroup's start over the workgroups; waves 0..15)")
+            for j, name in WAVE_PHASES:
+                m = W[:, :, j] > 0
+                if m.any():
+                    t = np.where(m, (W[:, :, j] - C[:, 0:1]) / ticks_per_ns, np.nan)
+                    with np.errstate(all="ignore"), warnings.catch_warnings():
+                        warnings.simplefilter("ignore", RuntimeWarning)  # waves that never stamp j
+                        med = np.nanmedian(t, axis=0)
+                    print(f"{name:22s} " + " ".join("    -" if np.isnan(x) else f"{x:5.0f}" for x in med))
     cand = C[:, 14][C[:, 14] > 0]
     if cand.size:
         print(f"candidates per workgroup: min {cand.min()} median {np.median(cand):.0f} max {cand.max()}")
@@ -357,10 +370,11 @@ def main(argv=None) -> int:
     ph.add_argument("--k", type=int, default=50)
     ph.add_argument("--b2b", type=int, default=20)
     ph.add_argument("--shape", default=None, help="SEGxLEN of N(0,1) fp16 instead of a workload")
+    ph.add_argument("--per-wave", action="store_true", help="also the median of every wave step by wave index")
     a = ap.parse_args(argv)
 
     if a.cmd == "phases":
-        run_phases(a.workload, a.k, a.b2b, a.shape)
+        run_phases(a.workload, a.k, a.b2b, a.shape, a.per_wave)
         return 0
 
     if a.cmd == "floor":
