@@ -39,6 +39,43 @@ __global__ void __launch_bounds__(BLOCK) read_floor_kernel(const uint16_t* in, i
   if ((threadIdx.x & 63) == 0) out[blockIdx.x * (BLOCK / 64) + (threadIdx.x >> 6)] = m;
 }
 
+// The same read with one 1024-thread workgroup per row and 16 vectors per thread, stamping
+// per wave (lane 0, shader clock) its start, the moment its 16 loads are issued and the moment
+// all its data is in (after a dependent reduction), into stamps[(row * 16 + wave) * 3 + i].
+// `barrier_first` adds a workgroup barrier before the loads.  Shows in what order a CU serves
+// the loads of its waves.
+__device__ __forceinline__ unsigned long long shader_clock() {
+  unsigned long long t;
+  asm volatile("s_memtime %0\n s_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
+  return t;
+}
+__global__ void __launch_bounds__(1024) arrival_kernel(const uint16_t* in, int row_len, int barrier_first,
+                                                       unsigned* out, unsigned long long* stamps) {
+  const unsigned long long c0 = shader_clock();
+  const unsigned char* base = reinterpret_cast<const unsigned char*>(in + static_cast<size_t>(blockIdx.x) * row_len);
+  if (barrier_first) __syncthreads();
+  u32x4_t v[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    int pos = (j * 1024 + static_cast<int>(threadIdx.x)) * 8;
+    if (pos + 8 > row_len) pos = 0;
+    v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + pos * 2));
+  }
+  const unsigned long long c1 = shader_clock();
+  unsigned m = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) m = max(m, max(max(v[j].x, v[j].y), max(v[j].z, v[j].w)));
+  m = max(m, static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(m), 63)));
+  const unsigned long long c2 = shader_clock();
+  if ((threadIdx.x & 63) == 0) {
+    const int wv = static_cast<int>(blockIdx.x) * 16 + static_cast<int>(threadIdx.x >> 6);
+    out[wv] = m;
+    stamps[wv * 3 + 0] = c0;
+    stamps[wv * 3 + 1] = c1;
+    stamps[wv * 3 + 2] = c2;
+  }
+}
+
 // A kernel that does nothing: the launch cost alone.
 __global__ void __launch_bounds__(1024) empty_kernel(unsigned* out) {
   if (threadIdx.x == 0x7fffffff) out[0] = 1;
@@ -72,6 +109,19 @@ extern "C" int read_floor_run(const uint16_t* const* inputs, int calls, int rows
     if (rc != 0) return rc;
   }
   return 0;
+}
+
+// `calls` back-to-back launches of the arrival kernel over inputs[i] (rows of row_len fp16, at
+// most 131,072); the stamps of the last launch stay in `stamps` (rows * 16 * 3 words), `out`
+// needs rows * 16 words.
+extern "C" int read_floor_arrival_run(const uint16_t* const* inputs, int calls, int rows, int row_len,
+                                      int barrier_first, unsigned* out, unsigned long long* stamps, void* stream) {
+  if (row_len <= 0 || row_len > 1024 * 16 * 8) return static_cast<int>(hipErrorInvalidValue);
+  for (int i = 0; i < calls; ++i) {
+    hipLaunchKernelGGL(arrival_kernel, dim3(static_cast<unsigned>(rows)), dim3(1024), 0,
+                       static_cast<hipStream_t>(stream), inputs[i], row_len, barrier_first, out, stamps);
+  }
+  return static_cast<int>(hipGetLastError());
 }
 
 // `calls` back-to-back launches of an empty kernel with `rows` workgroups of 1024 threads.

@@ -19,7 +19,8 @@
 
   python -m batch_topk_amd.profiling floor [--calls 2000]
       Back-to-back time of the single-pass read floor (libread_floor.so) over the 128 x 128,256
-      fp16 batch, rotating over 17 input copies (557 MB), for several workgroup shapes.
+      fp16 batch, rotating over 17 input copies (557 MB), for several workgroup shapes; the
+      per-wave arrival order of one workgroup's loads; the asymptotic streaming rate.
 
   python -m batch_topk_amd.profiling matrix [--out FILE]
       bench.py over every workload (fp16; bf16 and the sampling consumer on the LLM logits;
@@ -131,6 +132,26 @@ def run_floor(calls: int) -> None:
         torch.cuda.synchronize()
         us = a.elapsed_time(b) * 1e3 / calls
         print(f"{w} | {block} x {vpt} | {us:.2f} | {nbytes / us / 1e3:.0f} | {nbytes / us / 1e3 / 8000:.3f}")
+    # Per-wave arrival: in what order one CU serves the loads of a 1024-thread workgroup.
+    lib.read_floor_arrival_run.restype = i32
+    lib.read_floor_arrival_run.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp]
+    stamps = torch.zeros(rows * 16 * 3, dtype=torch.int64, device="cuda:0")
+    aout = torch.empty(rows * 16, dtype=torch.int32, device="cuda:0")
+    print("per-wave arrival, 1 workgroup of 1024 threads x 16 vectors per row (median over the "
+          f"{rows} workgroups of the last of 200 back-to-back launches; ns from the workgroup's first wave start)")
+    for barrier_first in (0, 1):
+        rc = lib.read_floor_arrival_run(ptrs, 200, rows, row_len, barrier_first, aout.data_ptr(),
+                                        stamps.data_ptr(), stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"read_floor_arrival_run returned {rc}")
+        torch.cuda.synchronize()
+        S = stamps.view(rows, 16, 3).cpu().numpy().astype(np.int64)
+        # the shader clock runs at about 2.4 GHz on this part
+        rel = (S - S[:, :, 0].min(axis=1)[:, None, None]) / 2.4
+        print(f"{'barrier before the loads' if barrier_first else 'no barrier'}: wave | "
+              + " ".join(f"{w:5d}" for w in range(16)))
+        for col, name in ((0, "start"), (1, "loads issued"), (2, "data in")):
+            print(f"  {name:12s} | " + " ".join(f"{x:5.0f}" for x in np.median(rel[:, :, col], axis=0)))
     # Asymptotic streaming rate: the same loads over 512 MiB per launch (2048 rows of 131,072
     # fp16, two buffers alternating), where the launch cost and the ramp are a few percent.
     big_rows, big_len = 2048, 131072
