@@ -703,6 +703,85 @@ __device__ __forceinline__ void sort_rank_write(const TopkParams& p, int64_t n, 
   }
 }
 
+// The same network on one u32 per lane: a step is one lane move and a min, a max and a select
+// (the u64 form needs two moves, a 64-bit compare and two selects).
+template <int M, int HI>
+__device__ __forceinline__ u32 sort_step32(u32 x, int lane) {
+  const u32 y = xor_lane<M>(x, lane);
+  const u32 lo = x < y ? x : y;
+  const u32 hi = x < y ? y : x;
+  return (lane & HI) ? hi : lo;
+}
+__device__ __forceinline__ u32 wave_sort64_u32(u32 x, int lane) {
+  x = sort_step32<1, 1>(x, lane);
+  x = sort_step32<3, 2>(x, lane);
+  x = sort_step32<1, 1>(x, lane);
+  x = sort_step32<7, 4>(x, lane);
+  x = sort_step32<2, 2>(x, lane);
+  x = sort_step32<1, 1>(x, lane);
+  x = sort_step32<15, 8>(x, lane);
+  x = sort_step32<4, 4>(x, lane);
+  x = sort_step32<2, 2>(x, lane);
+  x = sort_step32<1, 1>(x, lane);
+  x = sort_step32<31, 16>(x, lane);
+  x = sort_step32<8, 8>(x, lane);
+  x = sort_step32<4, 4>(x, lane);
+  x = sort_step32<2, 2>(x, lane);
+  x = sort_step32<1, 1>(x, lane);
+  x = sort_step32<63, 32>(x, lane);
+  x = sort_step32<16, 16>(x, lane);
+  x = sort_step32<8, 8>(x, lane);
+  x = sort_step32<4, 4>(x, lane);
+  x = sort_step32<2, 2>(x, lane);
+  x = sort_step32<1, 1>(x, lane);
+  return x;
+}
+
+// sort_rank_write for 16-bit candidates of a segment shorter than 65,535 elements: every
+// candidate is ordered by the u32 key16 << 16 | index16 (unique, and never the padding ~0), so
+// the runs are sorted and searched as u32 in `runs` (free LDS of M + 64 words); each thread
+// keeps its u64 candidate for the output.
+template <int BLOCK, class E>
+__device__ __forceinline__ void sort_rank_write16(const TopkParams& p, int64_t n, int seg, const u64* list, int M,
+                                                  int kk, u64* sorted, u32* runs) {
+  constexpr int NW = BLOCK / 64;
+  static_assert(NW <= 16, "at most 16 runs");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int R = (M + 63) >> 6;  // runs
+  const u64 P = tid < M ? list[tid] : ~0ull;
+  const u32 x = tid < M ? ((static_cast<u32>(P >> 48) << 16) | (static_cast<u32>(P >> 16) & 0xffffu)) : ~0u;
+  if (wid < R) runs[tid] = wave_sort64_u32(x, lane);
+  __syncthreads();
+  if (tid < M) {
+    int r = 0;
+    for (int b0 = 0; b0 < R; b0 += 8) {  // uniform
+      const u32* run[8];
+      int pos[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        run[i] = runs + 64 * (b0 + i < R ? b0 + i : wid);  // past R: a real run, not counted
+        pos[i] = 0;
+      }
+#pragma unroll
+      for (int s = 32; s > 0; s >>= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pos[i] += run[i][pos[i] + s - 1] < x ? s : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pos[i] += run[i][pos[i]] < x ? 1 : 0;
+        r += b0 + i < R ? pos[i] : 0;
+      }
+    }
+    if (r < kk) {
+      write_rank<E>(p, n, seg, r, P);
+      if (sorted) sorted[r] = P;
+    }
+  }
+}
+
 // Ranks the M (<= 16 * S) unique candidates of `list` and writes those of rank < kk (also to
 // sorted[rank] when sorted is not null).  One DPP row (16 lanes) per candidate: lane q of the
 // row compares it with entries q, q + 16, ... (S of them, held in registers, loaded once), and
@@ -789,7 +868,9 @@ __device__ __forceinline__ void finalize_segment(const TopkParams& p, const Smem
     // sorted runs cost a fixed 21 DPP steps and 7 LDS levels.  Measured on 256 x 32000 fp16
     // rows of 256 distinct values: k = 256 (lists of about 370) 11.2 -> 9.4 us and k = 128
     // 9.5 -> 9.2 us with runs; with runs from 129 or 160 entries on, k = 64 lost 0.2-0.5 us.
-    if (M >= kSortRankMin) {
+    if (M >= kSortRankMin && E::kBytes == 2 && n < 0xffff) {
+      sort_rank_write16<BLOCK, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr, sm.stage);
+    } else if (M >= kSortRankMin) {
       sort_rank_write<BLOCK, E>(p, n, seg, sm.area, M, kk, sampling ? sorted : nullptr);
     } else if (E::kBytes == 2 && n <= 0x10000) {
       lds_rank_write16<BLOCK, E>(p, n, seg, sm.area, M, kk, sm.rank, sm.stage, sampling ? sorted : nullptr);
