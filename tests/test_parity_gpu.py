@@ -440,3 +440,28 @@ def test_bf16_torch_convenience():
     assert vals.dtype == torch.bfloat16
     assert np.array_equal(idx.cpu().numpy(), ei)
     assert np.array_equal(vals.view(torch.int16).cpu().numpy().view(np.uint16), ev)
+
+
+# Lists of 256 to 512 candidates are ranked by sorted runs: on u32 keys (key16 << 16 | index16)
+# in 16-bit rows shorter than 65,535 elements, on the u64 candidates otherwise.  Both sides of
+# that bound, fp16 and bf16, on rows of 512 distinct values (about 128 copies of each, so the
+# threshold's ties make lists of 350-400), with NaNs and -inf at the last positions.
+@pytest.mark.parametrize("seg_len", [65533, 65534, 65535, 65536])
+@pytest.mark.parametrize("fmt", ["f16", "bf16"])
+def test_sorted_runs_index_bound(seg_len, fmt):
+    rng = np.random.default_rng(seg_len)
+    v = (rng.integers(0, 512, size=(3, seg_len)) - 256) / 64.0
+    if fmt == "f16":
+        bits = v.astype(np.float16).view(np.uint16)
+        nan, ninf = 0x7E00, 0xFC00
+    else:
+        bits = to_bf16_bits(v)
+        nan, ninf = 0x7FC0, 0xFF80
+    bits[:, -1] = nan
+    bits[:, -2] = ninf
+    bits[1, -3] = nan | 0x8000
+    what = f"sorted runs at the index bound {seg_len} {fmt}"
+    announce(f"{what} k=300")
+    got = run_fixed(bits, 300, fmt=fmt)
+    exp = O.batch_topk_half(bits, 300, seg_len=seg_len, threads=THREADS, fmt=fmt)
+    assert_same(got, exp, what)
