@@ -38,8 +38,8 @@ constexpr int kMaxChunk = 1024 * 16 * 8;
 //   lists   u64 [W][kCandArea]        every workgroup's candidate list
 constexpr int kRefineDigits = 8;
 constexpr int kGroupBarriers = 3 + kRefineDigits;
-constexpr int kGroupCopies = 16;
-constexpr int kFineCopies = 8;
+constexpr int kGroupCopies = 4;
+constexpr int kFineCopies = 4;
 constexpr int kFineBins = 2048;
 // Longest whole-segment list the final ranking takes: it is gathered into the LDS from the
 // candidate area onward (area, selection, rank and staging regions, free by then), which

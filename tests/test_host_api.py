@@ -111,7 +111,7 @@ def test_noalloc_entry_point_rejects_before_any_hip_call():
     assert call(P_IN, 1, 10, 11, P_VAL, P_IDX) == INVALID
     assert call(P_IN, 0, 10000, 50, P_VAL, P_IDX) == INVALID
     assert call(P_IN, 1, 10000, bt.MAX_K + 1, P_VAL, P_IDX) == INVALID
-    big = (100, 20_000_000, 64)
+    big = (128, 16_000_000, 64)
     assert bt.batch_topk_half_workspace_size(*big) > bt.NOALLOC_SCRATCH_BYTES
     assert call(P_IN, *big, P_VAL, P_IDX) == bt.HIP_ERROR_OUT_OF_MEMORY
     # the workloads of the benchmark fit it
