@@ -387,7 +387,7 @@ def test_bf16_random_with_specials(seg_num, seg_len, k):
 
 
 def test_bf16_llm_logits_full():
-    # The C2 logits (128 x 128,256, N(0, sd 2) with a +8 boosted tail) rounded to bfloat16.
+    # The LLM-logits rows (128 x 128,256, N(0, sd 2) with a +8 boosted tail) rounded to bfloat16.
     bits = to_bf16_bits(wl.llm_logits().view(np.float16).astype(np.float32))
     vals, idx = check_bf16(bits, 50, "llm_logits")
     assert_properties(bits, vals, idx, 50, [bits.shape[1]] * bits.shape[0], fmt="bf16")
