@@ -145,6 +145,40 @@ def test_f32_plan_branches_with_special_rows(seg_num, seg_len, k):
     check(bits, k, f"plan branch {seg_num}x{seg_len}", elem_offset=1)
 
 
+def _f32_kind(kind, rng, n):
+    if kind == "ties":  # 13 distinct values
+        x = (rng.integers(-6, 7, size=n) * 0.25).astype(np.float32)
+    elif kind == "sorted":  # every top value in the last chunk
+        x = np.sort(rng.standard_normal(n).astype(np.float32))
+    elif kind == "descending":  # every top value in the first chunk
+        x = -np.sort(rng.standard_normal(n).astype(np.float32))
+    elif kind == "nan_inf":  # NaNs with random payloads, -inf and a few +inf among normals
+        x = rng.standard_normal(n).astype(np.float32)
+        r = rng.random(n)
+        x[r < 0.3] = np.nan
+        x[(r >= 0.3) & (r < 0.5)] = -np.inf
+        x[r > 0.99995] = np.inf
+    else:
+        raise KeyError(kind)
+    bits = x.view(np.uint32).copy()
+    if kind == "nan_inf":
+        nan = np.isnan(x)
+        bits[nan] = 0x7F800001 | rng.integers(0, 2**22, size=int(nan.sum())).astype(np.uint32)
+    return bits
+
+
+# the cooperative path (segments over many co-resident workgroups) on tied, ordered and
+# NaN-heavy fp32 rows: 32-bit keys take up to 8 refinement digits when the lists overflow
+@pytest.mark.parametrize("seg_num,seg_len,k,kind", [
+    (1, 1_000_000, 1024, "ties"), (1, 1_000_000, 1024, "sorted"), (1, 1_000_000, 1024, "descending"),
+    (1, 1_000_000, 1024, "nan_inf"), (2, 3_000_000, 64, "ties"), (2, 3_000_000, 64, "sorted"),
+])
+def test_f32_cooperative_data_kinds(seg_num, seg_len, k, kind):
+    rng = np.random.default_rng(seg_len + k)
+    bits = _f32_kind(kind, rng, seg_num * seg_len).reshape(seg_num, seg_len)
+    check(bits, k, f"cooperative {kind} {seg_num}x{seg_len}")
+
+
 def test_f32_ex_flags_and_torch_mirror():
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(21)
