@@ -58,13 +58,13 @@ Plan make_plan(int seg_num, int64_t max_len, int k, int ev = 8, bool shared_alig
   int block = 1024, vpt = 16;
   bool found = false;
   if (seg_num >= 2 * kPlanCUs) {
-    // More segments than two per CU: the fewest threads (at least 512; 256 for 16-bit rows
-    // that 256 threads x 4 vectors cover) whose chunk covers max_len, so that several
-    // workgroups share a CU and one's loads overlap another's selection.  A segment whose
-    // misaligned span reaches past the chunk takes a second (tail) workgroup.  (256 threads
-    // for 10,000-element rows were faster on N(0,1) rows but slower on the reference bench's
-    // pattern, whose period divides their 2,048-element vector stride.)
-    const int many_min = (ev == 8 && max_len <= 256 * 4 * ev) ? 256 : 512;
+    // More segments than two per CU: the fewest threads (at least 512; 256 for rows that 256
+    // threads x 4 vectors cover) whose chunk covers max_len, so that several workgroups share
+    // a CU and one's loads overlap another's selection.  A segment whose misaligned span
+    // reaches past the chunk takes a second (tail) workgroup.  (256 threads for 10,000-element
+    // fp16 rows were faster on N(0,1) rows but slower on the reference bench's pattern, whose
+    // period divides their 2,048-element vector stride.)
+    const int many_min = max_len <= 256 * 4 * ev ? 256 : 512;
     for (int cb = block_min > many_min ? block_min : many_min; cb <= 1024 && !found; cb *= 2) {
       for (int cv : {2, 4, 8, 16}) {
         if (!found && static_cast<int64_t>(cb) * cv * ev >= max_len) {
