@@ -220,3 +220,28 @@ def test_f32_huge_segment_uses_every_cu_when_aligned():
     rc = bt.batch_topk_f32(buf.data_ptr() + 4, 1, n, 1024, vals.data_ptr(), idx.data_ptr(),
                            ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
     assert rc == 720
+
+
+# the many-row plan (at least 512 rows): 256-thread workgroups for rows of at most 4,096
+# floats, 512 threads above; misaligned starts give some rows a tail workgroup
+@pytest.mark.parametrize("seg_num,seg_len,k,kind", [
+    (2000, 2000, 50, None), (4096, 1024, 64, "ties"), (1000, 4096, 50, "nan_inf"),
+    (700, 4097, 50, None), (600, 4096, 1, "sorted"), (512, 3000, 128, "descending"),
+])
+def test_f32_many_row_plan(seg_num, seg_len, k, kind):
+    rng = np.random.default_rng(seg_num + seg_len + k)
+    n = seg_num * seg_len
+    bits = (rng.standard_normal(n).astype(np.float32).view(np.uint32) if kind is None
+            else _f32_kind(kind, rng, n)).reshape(seg_num, seg_len)
+    check(bits, k, f"many-row plan {seg_num}x{seg_len} {kind}", elem_offset=3)
+
+
+@pytest.mark.parametrize("seg_num,max_len,k", [(1000, 4096, 50), (3000, 2048, 16), (800, 5000, 64)])
+def test_f32_many_row_segmented(seg_num, max_len, k):
+    rng = np.random.default_rng(seg_num * 7 + max_len)
+    lengths = rng.integers(0, max_len + 1, size=seg_num).astype(np.int64)
+    lengths[:4] = [0, 1, max_len, k]
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    bits = rng.standard_normal(int(offsets[-1])).astype(np.float32).view(np.uint32)
+    check(bits, k, f"many-row segmented {seg_num} x U[0,{max_len}]", offsets=offsets, max_len=max_len,
+          elem_offset=1)
