@@ -59,12 +59,12 @@ Plan make_plan(int seg_num, int64_t max_len, int k, int ev = 8, bool shared_alig
   bool found = false;
   if (seg_num >= 2 * kPlanCUs) {
     // More segments than two per CU: the fewest threads (at least 512; 256 for rows that 256
-    // threads x 4 vectors cover) whose chunk covers max_len, so that several workgroups share
+    // threads x 8 vectors cover) whose chunk covers max_len, so that several workgroups share
     // a CU and one's loads overlap another's selection.  A segment whose misaligned span
-    // reaches past the chunk takes a second (tail) workgroup.  (256 threads for 10,000-element
-    // fp16 rows were faster on N(0,1) rows but slower on the reference bench's pattern, whose
-    // period divides their 2,048-element vector stride.)
-    const int many_min = max_len <= 256 * 4 * ev ? 256 : 512;
+    // reaches past the chunk takes a second (tail) workgroup.  (Longer rows on 256 threads
+    // take 16 vectors per thread, whose per-wave chains cost more than the extra workgroups
+    // gain: 1,024 x 30,000 ran 14.39 us on 512 threads and 14.92 on 256.)
+    const int many_min = max_len <= 256 * 8 * ev ? 256 : 512;
     for (int cb = block_min > many_min ? block_min : many_min; cb <= 1024 && !found; cb *= 2) {
       for (int cv : {2, 4, 8, 16}) {
         if (!found && static_cast<int64_t>(cb) * cv * ev >= max_len) {

@@ -1273,6 +1273,18 @@ segmented_topk_kernel(TopkParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = tid >> 6;
+  // Vector slot of thread tid's vector j: in block j of BLOCK vectors, slot tid rotated by
+  // ROT * j.  A rotation by a multiple of 64 keeps each wave's 64 slots contiguous and leaves
+  // block 0 as it is.  Without it, data whose period divides the BLOCK * EV-element block
+  // stride (the reference bench's fill repeats every 2,048 elements) gives a thread the same
+  // values in every vector, its best then summarises one vector, and the threshold from the
+  // thread bests lets several times k candidates through (1,500 rows of 10,000 such elements:
+  // 371 candidates a row against 53 on random data).  Only the one-workgroup-per-chunk kernels
+  // of at most 8 vectors rotate: the 16-vector ones serve rows long enough that the threshold
+  // comes from many distinct vectors anyway.
+  constexpr int ROT = (!COOP && VPT <= 8) ? 64 : 0;
+  auto vslot = [tid](int j) { return j * BLOCK + ((tid + ROT * j) & (BLOCK - 1)); };
+  auto wslot = [wid](int j) { return j * BLOCK + ((wid * 64 + ROT * j) & (BLOCK - 1)); };
   const int W = p.chunks_per_seg;
   // Chunk-major grid: every segment's first chunk is dispatched before any second chunk, so
   // the workgroups of chunks a segment does not reach (they return at once) come last.
@@ -1358,10 +1370,11 @@ segmented_topk_kernel(TopkParams p) {
   }
 
   // ---- 1. load the chunk: all nontemporal 16-byte loads issued before any is consumed.
-  // Buffer loads from the chunk's base: vector j of thread tid is at byte tid * 16 (one VGPR
-  // for every j) plus j * BLOCK * 16 (a scalar offset).  The buffer ends at the first 8-block
-  // boundary at or past hi, so a vector wholly past the chunk reads as zero without touching
-  // memory; the vector holding hi is read whole, as the refinement re-read below also does.
+  // Buffer loads from the chunk's base: vector j of thread tid is at byte
+  // ((tid + ROT * j) mod BLOCK) * 16 (a VGPR) plus j * BLOCK * 16 (a scalar offset).  The
+  // buffer ends at the first 8-block boundary at or past hi, so a vector wholly past the chunk
+  // reads as zero without touching memory; the vector holding hi is read whole, as the
+  // refinement re-read below also does.
   uint4 v[VPT];
   const unsigned char* cptr = reinterpret_cast<const unsigned char*>(p.base) + cb * E::kBytes;
   {
@@ -1370,7 +1383,7 @@ segmented_topk_kernel(TopkParams p) {
         kBufferWord3);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, tid * 16, j * BLOCK * 16, kCachePolicyNT);
+      const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (vslot(j) - j * BLOCK) * 16, j * BLOCK * 16, kCachePolicyNT);
       v[j] = make_uint4(t.x, t.y, t.z, t.w);
     }
   }
@@ -1400,7 +1413,7 @@ segmented_topk_kernel(TopkParams p) {
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     if ((j == 0 && lo > 0) || (j + 1) * BLOCK * EV > hi) {
-      const int pos = (j * BLOCK + tid) * EV;
+      const int pos = vslot(j) * EV;
       if (pos < lo || pos + EV > hi) {
         u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
@@ -1486,7 +1499,7 @@ segmented_topk_kernel(TopkParams p) {
             for (int e = 0; e < EV; ++e) {
               const u32 b = E::element(w4, e);
               if (b - t_lo <= span) {  // t_lo <= b <= inf, as unsigned
-                const u64 P = (static_cast<u64>(b ^ 0x7fffu) << 32) | static_cast<u32>((j * BLOCK + tid) * EV + e);
+                const u64 P = (static_cast<u64>(b ^ 0x7fffu) << 32) | static_cast<u32>(vslot(j) * EV + e);
                 mine = P < mine ? P : mine;
               }
             }
@@ -1718,7 +1731,7 @@ segmented_topk_kernel(TopkParams p) {
         if (mine) {
           const u32 slot = nst + mbcnt(m);
           st_vec[slot] = v[j];
-          st_pos[slot] = static_cast<u32>((j * BLOCK + tid) * EV);
+          st_pos[slot] = static_cast<u32>(vslot(j) * EV);
         }
         nst += c;
       }
@@ -1742,7 +1755,7 @@ segmented_topk_kernel(TopkParams p) {
     for (int j = 0; j < VPT; ++j) {
       // the wave's positions of vector j: skip the whole vector (wave-uniform) when none
       // is in [lo, hi), as in every vector of a short segment past its end
-      const int wpos = (j * BLOCK + wid * 64) * EV;
+      const int wpos = wslot(j) * EV;
       if (wpos >= hi || wpos + 64 * EV <= lo) continue;
       const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
@@ -1759,7 +1772,7 @@ segmented_topk_kernel(TopkParams p) {
           if (h) {
             const u32 slot = wcount + mbcnt(m);
             if (slot < static_cast<u32>(RC))
-              region[slot] = E::pack(b, idx_base + static_cast<u32>((j * BLOCK + tid) * EV + e), inf);
+              region[slot] = E::pack(b, idx_base + static_cast<u32>(vslot(j) * EV + e), inf);
           }
           wcount += static_cast<u32>(__popcll(m));
         }
@@ -1794,7 +1807,7 @@ segmented_topk_kernel(TopkParams p) {
   auto for_each_element = [&](auto&& fn) {
 #pragma unroll 1
     for (int j = 0; j < VPT; ++j) {
-      const int pos0 = (j * BLOCK + tid) * EV;
+      const int pos0 = vslot(j) * EV;
       if (pos0 < hi && pos0 + EV > lo) {
         const uint4 x = *reinterpret_cast<const uint4*>(cptr + static_cast<u32>(pos0) * E::kBytes);
         const u32 w4[4] = {x.x, x.y, x.z, x.w};
@@ -1906,12 +1919,12 @@ segmented_topk_kernel(TopkParams p) {
     // holds no position of [lo, hi) are skipped as a whole (wave-uniform).
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int wpos = (j * BLOCK + wid * 64) * EV;
+      const int wpos = wslot(j) * EV;
       if (wpos >= hi || wpos + 64 * EV <= lo) continue;
       const u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
       for (int e = 0; e < EV; ++e) {
-        const int pos = (j * BLOCK + tid) * EV + e;
+        const int pos = vslot(j) * EV + e;
         const u32 b = E::element(w4, e);
         if (pos >= lo && pos < hi) sm.area[pos - lo] = E::pack(b, idx_base + static_cast<u32>(pos), inf);
       }
