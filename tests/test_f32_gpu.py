@@ -222,11 +222,13 @@ def test_f32_huge_segment_uses_every_cu_when_aligned():
     assert rc == 720
 
 
-# the many-row plan (at least 512 rows): 256-thread workgroups for rows of at most 4,096
-# floats, 512 threads above; misaligned starts give some rows a tail workgroup
+# the many-row plan (at least 512 rows): 256-thread workgroups for rows of at most 8,192
+# floats (8 vectors per thread), 512 threads above; misaligned starts give some rows a tail
+# workgroup
 @pytest.mark.parametrize("seg_num,seg_len,k,kind", [
     (2000, 2000, 50, None), (4096, 1024, 64, "ties"), (1000, 4096, 50, "nan_inf"),
     (700, 4097, 50, None), (600, 4096, 1, "sorted"), (512, 3000, 128, "descending"),
+    (1000, 8192, 64, "ties"), (600, 8193, 50, None),
 ])
 def test_f32_many_row_plan(seg_num, seg_len, k, kind):
     rng = np.random.default_rng(seg_num + seg_len + k)
