@@ -59,12 +59,16 @@ Plan make_plan(int seg_num, int64_t max_len, int k, int ev = 8, bool shared_alig
   bool found = false;
   if (seg_num >= 2 * kPlanCUs) {
     // More segments than two per CU: the fewest threads (at least 512; 256 for rows that 256
-    // threads x 8 vectors cover) whose chunk covers max_len, so that several workgroups share
-    // a CU and one's loads overlap another's selection.  A segment whose misaligned span
-    // reaches past the chunk takes a second (tail) workgroup.  (Longer rows on 256 threads
-    // take 16 vectors per thread, whose per-wave chains cost more than the extra workgroups
-    // gain: 1,024 x 30,000 ran 14.39 us on 512 threads and 14.92 on 256.)
-    const int many_min = max_len <= 256 * 8 * ev ? 256 : 512;
+    // threads x 4 vectors cover, or x 8 vectors from three segments per CU on) whose chunk
+    // covers max_len, so that several workgroups share a CU and one's loads overlap another's
+    // selection.  A segment whose misaligned span reaches past the chunk takes a second (tail)
+    // workgroup.  (With fewer segments, 8-vector rows on 256 threads leave too few waves per
+    // CU: 512 x 12,000 ran 7.14 us on 512 threads and 7.62 on 256, while 800 x 12,000 ran 10.14
+    // and 9.08.  Longer rows on 256 threads take 16 vectors per thread, whose per-wave chains
+    // cost more than the extra workgroups gain: 1,024 x 30,000 ran 14.39 us on 512 threads
+    // and 14.92 on 256.)
+    const bool many_short = max_len <= 256 * 4 * ev || (max_len <= 256 * 8 * ev && seg_num >= 3 * kPlanCUs);
+    const int many_min = many_short ? 256 : 512;
     for (int cb = block_min > many_min ? block_min : many_min; cb <= 1024 && !found; cb *= 2) {
       for (int cv : {2, 4, 8, 16}) {
         if (!found && static_cast<int64_t>(cb) * cv * ev >= max_len) {
