@@ -222,9 +222,9 @@ def test_f32_huge_segment_uses_every_cu_when_aligned():
     assert rc == 720
 
 
-# the many-row plan (at least 512 rows): 256-thread workgroups for rows of at most 8,192
-# floats (8 vectors per thread), 512 threads above; misaligned starts give some rows a tail
-# workgroup
+# the many-row plan (at least 512 rows): 256-thread workgroups for rows of at most 4,096
+# floats, and of at most 8,192 (8 vectors per thread) from 768 rows on; 512 threads otherwise
+# (700 x 4,097 and 600 x 8,193 here); misaligned starts give some rows a tail workgroup
 @pytest.mark.parametrize("seg_num,seg_len,k,kind", [
     (2000, 2000, 50, None), (4096, 1024, 64, "ties"), (1000, 4096, 50, "nan_inf"),
     (700, 4097, 50, None), (600, 4096, 1, "sorted"), (512, 3000, 128, "descending"),
