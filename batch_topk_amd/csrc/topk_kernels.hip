@@ -1413,14 +1413,23 @@ segmented_topk_kernel(TopkParams p) {
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     if ((j == 0 && lo > 0) || (j + 1) * BLOCK * EV > hi) {
-      const int pos = vslot(j) * EV;
-      if (pos < lo || pos + EV > hi) {
-        u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      if (BLOCK <= 512 && j * BLOCK * EV >= hi) {
+        // The whole block lies past the chunk (short rows of a batch planned for its longest,
+        // the last blocks of a 10,000-element row on 256 x 8): the filler (all ones in every
+        // format), with no per-lane test.  1024-thread kernels keep the one path: their
+        // chunks rarely end a block early, and the extra branch cost 256 x 32,000 rows about
+        // 0.1 us.
+        v[j] = make_uint4(~0u, ~0u, ~0u, ~0u);
+      } else {
+        const int pos = vslot(j) * EV;
+        if (pos < lo || pos + EV > hi) {
+          u32 w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-        for (int e = 0; e < EV; ++e) {
-          if (pos + e < lo || pos + e >= hi) E::fill(w4, e);
+          for (int e = 0; e < EV; ++e) {
+            if (pos + e < lo || pos + e >= hi) E::fill(w4, e);
+          }
+          v[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         }
-        v[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
       }
     }
   }
